@@ -1,0 +1,209 @@
+/*
+ * mi_hip_attn.h -- C ABI of the MI355X (gfx950) batched GQA attention
+ * backend for the mini-infer engine.
+ *
+ * What it replaces: the three CPU graph ops
+ *   MI_OP_ATTN_QK   src/ops_cpu.cpp:356-380  (scores  S[i,j,h] = K[:,h/n_rep,i].Q[:,h,j])
+ *   MI_OP_SOFTMAX   src/ops_cpu.cpp:304-346  (causal, scaled, per (j,h) row)
+ *   MI_OP_ATTN_KQV  src/ops_cpu.cpp:386-410  (O[o,h,j] = sum_t V[o,h/n_rep,t].P[t,j,h])
+ * plus the KV cache that feeds them (src/model_qwen2.cpp:557-596, the K/V
+ * append CPY nodes of src/model_qwen2.cpp:156-159) and the per-node dispatch
+ * point of the executor (src/ops_cpu.cpp:481-530, src/threadpool.cpp:171-180).
+ *
+ * Conventions
+ *   - Every function returns an int status (MI_HIP_OK == 0). It never throws
+ *     and never aborts on bad arguments; the message of the last failure on
+ *     the calling thread is returned by mi_hip_last_error().
+ *   - Layouts are the engine's: Q and O are [head_dim, n_head, n_tokens], the
+ *     K and V caches are [head_dim, n_head_kv, n_ctx] per layer, ne[0]
+ *     innermost, strides in bytes. Q head h reads KV head h / n_rep: GQA is an
+ *     index mapping, no K/V row is ever copied per head.
+ *   - Pointers named "device" must be device (HBM) addresses; "host" pointers
+ *     are ordinary host memory.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the null stream.
+ *     Calls enqueue work and return; the caller synchronises the stream.
+ */
+#ifndef MI_HIP_ATTN_H
+#define MI_HIP_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "mi_tensor.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define MI_HIP_OK 0
+#define MI_HIP_E_INVALID 1     /* an argument is out of range or inconsistent */
+#define MI_HIP_E_NODEVICE 2    /* no usable gfx950 device */
+#define MI_HIP_E_RUNTIME 3     /* a HIP runtime call failed */
+#define MI_HIP_E_NOMEM 4       /* device allocation refused (or over the limit) */
+#define MI_HIP_E_UNSUPPORTED 5 /* valid request outside what the kernels cover */
+#define MI_HIP_E_STATE 6       /* called before mi_hip_init / on a dead object */
+
+/* ---- library lifetime -------------------------------------------------- */
+
+/* Selects `device` for this library and checks it is gfx950.
+ * Counterpart of the engine's one-time setup in mi_kv_cache_init
+ * (src/model_qwen2.cpp:557-596); idempotent for the same device. */
+int mi_hip_init(int device);
+
+/* Releases library-owned device memory (workspace). KV caches must have been
+ * destroyed by the caller first. */
+int mi_hip_shutdown(void);
+
+/* Thread-local text of the last failure ("" if none). */
+const char* mi_hip_last_error(void);
+
+/* Writes sizeof(mi_tensor), offsetof(type, ne, nb, op, op_params, src, data,
+ * view_src, view_offs, n_children, flags, name, extra) and sizeof(mi_cgraph)
+ * into out[0..14] (n >= 15) so a caller can verify it shares the layout of
+ * src/tensor.h:122-160 and src/graph.h:19-47. */
+int mi_hip_abi_layout(size_t* out, int n);
+
+/* ---- device allocation accounting -------------------------------------- */
+
+/* The engine forbids steady-state allocation (tests/test_zero_alloc.cpp).
+ * Every device allocation this library makes goes through one counter. */
+typedef struct mi_hip_alloc_stats {
+  uint64_t n_malloc;
+  uint64_t n_free;
+  uint64_t bytes_live;
+  uint64_t bytes_peak;
+} mi_hip_alloc_stats;
+
+int mi_hip_get_alloc_stats(mi_hip_alloc_stats* out);
+
+/* Caps the library's live device bytes (0 = no cap). An allocation that
+ * would exceed the cap fails with MI_HIP_E_NOMEM before calling HIP. */
+int mi_hip_set_alloc_limit(uint64_t bytes);
+
+/* ---- device-resident KV cache ------------------------------------------ */
+
+typedef struct mi_hip_kv mi_hip_kv;
+
+typedef struct mi_hip_kv_desc {
+  int32_t n_layer;
+  int32_t n_ctx;
+  int32_t n_head_kv;
+  int32_t head_dim;  /* 64 or 128 */
+  int32_t n_head;    /* Q heads (multiple of n_head_kv); sizes staging */
+  int32_t type;      /* MI_TYPE_F32 or MI_TYPE_F16 cache elements */
+} mi_hip_kv_desc;
+
+/* One device allocation holding every layer's K and V as
+ * [head_dim, n_head_kv, n_ctx] (position-major, the layout of
+ * src/model_qwen2.cpp:564-577), plus the split-KV workspace and the host-node
+ * staging buffers, all sized for n_ctx. Nothing is allocated afterwards.
+ * Replaces mi_kv_cache_init's host KV context (src/model_qwen2.cpp:564-577). */
+int mi_hip_kv_create(const mi_hip_kv_desc* desc, mi_hip_kv** out);
+int mi_hip_kv_destroy(mi_hip_kv* kv);
+
+/* Device view of one layer's cache: which = 0 for K, 1 for V. Fills the
+ * device address and the engine-style ne[4]/nb[4]. */
+int mi_hip_kv_view(mi_hip_kv* kv, int layer, int which, void** data, int64_t ne[4],
+                   size_t nb[4]);
+
+/* Writes n_tokens F32 rows src[head_dim, n_head_kv, n_tokens] (byte strides
+ * src_nb[0..2]) into positions [pos0, pos0 + n_tokens) of layer `layer`'s
+ * K (which = 0) or V (which = 1); F16 caches round to nearest even.
+ * src_on_device = 0 for a host source, 1 for a device source.
+ * This is the CPY-into-kv_write_view node (src/model_qwen2.cpp:99-103,
+ * 156-159; src/ops_cpu.cpp:446-460). Host sources are synchronous. */
+int mi_hip_kv_write(mi_hip_kv* kv, int layer, int which, int pos0, int n_tokens,
+                    const float* src, const size_t src_nb[3], int src_on_device,
+                    void* stream);
+
+/* Associates the engine's host KV tensor (the persistent leaf whose
+ * view_src-flattened views the CPY nodes write through, and which the
+ * ATTN_QK/ATTN_KQV nodes read as src[1]) with a layer of `kv`, for
+ * mi_hip_compute_forward. Keyed by the tensor's address, never by its
+ * `extra` field (the engine's allocator rewrites `extra` every step,
+ * src/gallocr.cpp:120-121). */
+int mi_hip_kv_bind(mi_hip_kv* kv, int layer, int which, const mi_tensor* host_kv);
+
+/* ---- fused attention ---------------------------------------------------- */
+
+typedef struct mi_hip_attn_args {
+  /* K/V source: either a cache + layer (kv != NULL) ... */
+  mi_hip_kv* kv;
+  int32_t layer;
+  /* ... or explicit device tensors [head_dim, n_head_kv, >= n_past+n_tokens]. */
+  const void* k;
+  const void* v;
+  size_t k_nb[3];
+  size_t v_nb[3];
+  int32_t kv_type;   /* MI_TYPE_F32 / MI_TYPE_F16 (explicit tensors only) */
+  int32_t head_dim;  /* explicit tensors only */
+  int32_t n_head_kv; /* explicit tensors only */
+  /* Queries: device [head_dim, n_head, n_tokens], byte strides q_nb. */
+  const float* q;
+  size_t q_nb[3];
+  /* Output: device [head_dim, n_head, n_tokens], byte strides out_nb. */
+  float* out;
+  size_t out_nb[3];
+  int32_t n_head;
+  int32_t n_rep;    /* n_head / n_head_kv (op_params[1] of ATTN_QK) */
+  int32_t n_past;   /* keys [0, n_past + j] visible to query j */
+  int32_t n_tokens; /* 1 = decode kernel, > 1 = prefill kernel */
+  float scale;      /* op_params[1] of SOFTMAX, 1/sqrt(head_dim) in the engine */
+  void* stream;
+} mi_hip_attn_args;
+
+/* The whole ATTN_QK -> causal SOFTMAX -> ATTN_KQV triple in one pass that
+ * never materialises scores or probabilities: the split-KV decode kernel when
+ * n_tokens == 1, the MFMA prefill kernel otherwise. Equivalent to running
+ * mi_compute_attn_qk, mi_compute_softmax and mi_compute_attn_kqv
+ * (src/ops_cpu.cpp:304-410) on the nodes built by src/model_qwen2.cpp:169-172,
+ * within floating-point tolerance. */
+int mi_hip_attn_fwd(const mi_hip_attn_args* args);
+
+/* n_items independent single-token decode problems of one shape (same
+ * head_dim, n_head, n_rep, K/V element type; n_past may differ) in ONE
+ * launch, e.g. many sequences' caches, or a stack of layers in a benchmark.
+ * No counterpart in the reference (it runs one node per layer). */
+int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* stream);
+
+/* ---- node-level operators on device tensors ----------------------------- */
+/*
+ * Same signature idea as the engine's kernels (src/ops_cpu.h:3-12): the node
+ * `dst` carries op, op_params and src[], and every tensor's `data` is a DEVICE
+ * address. Strides are honoured as in mi_f32_ptr (src/ops_cpu.cpp:38-41).
+ */
+
+/* MI_OP_ATTN_QK (src/ops_cpu.cpp:356-380; builder src/graph.cpp:241-253). */
+int mi_hip_op_attn_qk(mi_tensor* dst, void* stream);
+/* MI_OP_SOFTMAX (src/ops_cpu.cpp:304-346; builder src/graph.cpp:156-163). */
+int mi_hip_op_softmax(mi_tensor* dst, void* stream);
+/* MI_OP_ATTN_KQV (src/ops_cpu.cpp:386-410; builder src/graph.cpp:263-273). */
+int mi_hip_op_attn_kqv(mi_tensor* dst, void* stream);
+/* The fused triple given its last node: dst is the ATTN_KQV node,
+ * dst->src[0] the SOFTMAX node, dst->src[0]->src[0] the ATTN_QK node. */
+int mi_hip_op_attn_fused(mi_tensor* dst, void* stream);
+
+/* ---- executor hook for host-resident graphs ------------------------------ */
+
+/* Plans one step's graph (call after the allocator assigned data, before
+ * execution): marks every ATTN_QK -> SOFTMAX -> ATTN_KQV chain whose scores
+ * and probabilities have no other reader as fused. Allocation-free. */
+int mi_hip_graph_prepare(const mi_cgraph* graph);
+
+/* Drop-in for the dispatch in mi_compute_forward (src/ops_cpu.cpp:481-530),
+ * same (dst, ith, nth) contract as every engine kernel (src/ops_cpu.h:3-12)
+ * and the executor's per-node barrier (src/threadpool.cpp:171-180).
+ * Returns 1 if the node belongs to this backend (the caller then skips its CPU
+ * kernel), 0 if it does not, -1 on error (see mi_hip_last_error). Only ith == 0
+ * does work: it enqueues the node on the KV cache's stream and waits for it,
+ * so the node's host output is complete before the caller's barrier. Nodes
+ * handled: CPY into a bound KV tensor; ATTN_QK and SOFTMAX of a planned fused
+ * chain (no-ops); ATTN_KQV of a planned fused chain (the fused launch). */
+int mi_hip_compute_forward(mi_tensor* dst, int ith, int nth);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_HIP_ATTN_H */
