@@ -1,0 +1,302 @@
+"""Benchmark of the fused GQA attention kernels on one MI355X.
+
+Headline (one "step" = one pass of the hot path over one batch):
+  decode attention, 24 layers' independent caches at n_kv = 4096, Qwen2.5-0.5B
+  heads (14 Q / 2 KV, head_dim 64), F32 cache, one batched launch. `value` is
+  the algorithmic HBM bytes (K + V + Q + O) per step / time per step. Steps
+  rotate over several cache sets (> 256 MB in total) so reads come from HBM,
+  not the 256 MB Infinity Cache.
+Also reported (secondary, same run): prefill-1024 and -4096 causal attention
+TFLOP/s (causal FLOPs 4*D*H*n(n+1)/2), the Qwen2.5-7B-shape F16-cache decode
+at n_kv = 8192, and the engine's per-layer call pattern (24 single launches).
+The CPU baseline times the reference's three-node path (attn_qk -> softmax ->
+attn_kqv with a barrier per node) on the host cores on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "mini-infer-llama.cpp_amd")
+sys.path.insert(0, ROOT)
+sys.path.insert(0, PKG)
+
+METRIC = "decode attn GB/s (% HBM peak) @ n_kv=4096; prefill-1024 attn TFLOP/s"
+HBM_PEAK_GBPS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="", help="comma list: decode,prefill,d7b,perlayer")
+    return ap.parse_args()
+
+
+def decode_bytes(n_layers, n_kv, h, hkv, d, kv_elt):
+    return n_layers * (2 * n_kv * hkv * d * kv_elt + 2 * h * d * 4)
+
+
+def causal_flops(n, h, d):
+    return 4 * d * h * n * (n + 1) // 2
+
+
+class Timer:
+    """Per-launch HIP events on the stream the kernels run on."""
+
+    def __init__(self, torch, n):
+        self.torch = torch
+        self.ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                   for _ in range(n)]
+
+    def mean_ms(self):
+        return sum(a.elapsed_time(b) for a, b in self.ev) / len(self.ev)
+
+
+def run_timed(torch, launch, steps, warmup):
+    """warmup untimed steps, then `steps` timed steps bracketed by synchronize;
+    returns (ms per step over the region, mean per-launch event ms)."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    t = Timer(torch, steps)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        t.ev[i][0].record()
+        launch(i)
+        t.ev[i][1].record()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps, t.mean_ms()
+
+
+def bench_decode(torch, mh, lib, stream, steps, warmup, n_layers=24, n_kv=4096, h=14, hkv=2,
+                 d=64, f16=False, sets=None):
+    elt = 2 if f16 else 4
+    per_set = n_layers * 2 * n_kv * hkv * d * elt
+    if sets is None:
+        sets = max(3, -(-600 * 2**20 // per_set))  # > 256 MB MALL, about 600 MB rotated
+    gen = torch.Generator(device="cuda").manual_seed(4096)
+    dt = torch.float16 if f16 else torch.float32
+    arrays = []
+    for s in range(sets):
+        k = torch.randn((n_layers, n_kv, hkv, d), device="cuda", generator=gen).to(dt)
+        v = torch.randn((n_layers, n_kv, hkv, d), device="cuda", generator=gen).to(dt)
+        q = torch.randn((n_layers, 1, h, d), device="cuda", generator=gen)
+        o = torch.empty((n_layers, 1, h, d), device="cuda")
+        items = (mh.AttnArgs * n_layers)(*[
+            mh.attn_args(q[l], o[l], h // hkv, n_kv - 1, float(d) ** -0.5, stream, k=k[l], v=v[l])
+            for l in range(n_layers)])
+        arrays.append((k, v, q, o, items))
+
+    def launch(i):
+        items = arrays[i % sets][4]
+        rc = lib.mi_hip_attn_decode_batch(items, n_layers, stream)
+        if rc:
+            raise mh.MiHipError(rc, lib.last_error())
+
+    ms, kern_ms = run_timed(torch, launch, steps, warmup)
+    nbytes = decode_bytes(n_layers, n_kv, h, hkv, d, elt)
+    return dict(ms_per_step=ms, kernel_ms=kern_ms, bytes=nbytes, sets=sets,
+                gbps=nbytes / (ms * 1e-3) / 1e9, kernel_gbps=nbytes / (kern_ms * 1e-3) / 1e9)
+
+
+def bench_decode_per_layer(torch, mh, lib, stream, steps, warmup, n_layers=24, n_kv=4096):
+    """The engine's call pattern: one fused launch per layer node."""
+    h, hkv, d = 14, 2, 64
+    sets = 6
+    gen = torch.Generator(device="cuda").manual_seed(99)
+    per = []
+    for s in range(sets):
+        k = torch.randn((n_layers, n_kv, hkv, d), device="cuda", generator=gen)
+        v = torch.randn((n_layers, n_kv, hkv, d), device="cuda", generator=gen)
+        q = torch.randn((n_layers, 1, h, d), device="cuda", generator=gen)
+        o = torch.empty((n_layers, 1, h, d), device="cuda")
+        args = [mh.attn_args(q[l], o[l], 7, n_kv - 1, 0.125, stream, k=k[l], v=v[l])
+                for l in range(n_layers)]
+        per.append((k, v, q, o, args))
+
+    def launch(i):
+        for a in per[i % sets][4]:
+            rc = lib.mi_hip_attn_fwd(ctypes.byref(a))
+            if rc:
+                raise mh.MiHipError(rc, lib.last_error())
+
+    ms, _ = run_timed(torch, launch, max(5, steps // 4), max(2, warmup // 4))
+    nbytes = decode_bytes(n_layers, n_kv, h, hkv, d, 4)
+    return dict(us_per_layer=ms * 1e3 / n_layers, gbps=nbytes / (ms * 1e-3) / 1e9)
+
+
+def bench_prefill(torch, mh, lib, stream, steps, warmup, n, h=14, hkv=2, d=64):
+    gen = torch.Generator(device="cuda").manual_seed(n)
+    q = torch.randn((n, h, d), device="cuda", generator=gen)
+    k = torch.randn((n, hkv, d), device="cuda", generator=gen)
+    v = torch.randn((n, hkv, d), device="cuda", generator=gen)
+    o = torch.empty((n, h, d), device="cuda")
+    a = mh.attn_args(q, o, h // hkv, 0, float(d) ** -0.5, stream, k=k, v=v)
+
+    def launch(i):
+        rc = lib.mi_hip_attn_fwd(ctypes.byref(a))
+        if rc:
+            raise mh.MiHipError(rc, lib.last_error())
+
+    ms, kern_ms = run_timed(torch, launch, steps, warmup)
+    flops = causal_flops(n, h, d)
+    return dict(n=n, ms_per_step=ms, kernel_ms=kern_ms, flops=flops,
+                tflops=flops / (kern_ms * 1e-3) / 1e12)
+
+
+def cpu_baseline(n_layers_sample=24, n_kv=4096):
+    """The reference three-node CPU path on the host cores (bounded sample:
+    24 layers' decode attention at n_kv = 4096, 1 warmup + 7 timed passes)."""
+    import numpy as np
+    from oracle import cpu_attention
+    impl = cpu_attention.reference() or cpu_attention.oracle()
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(7)
+    qs = [rng.standard_normal((1, 14, 64), dtype=np.float32) for _ in range(n_layers_sample)]
+    ks = [rng.standard_normal((n_kv, 2, 64), dtype=np.float32) for _ in range(n_layers_sample)]
+    vs = [rng.standard_normal((n_kv, 2, 64), dtype=np.float32) for _ in range(n_layers_sample)]
+    t, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, threads, warmup=1, reps=7)
+    nbytes = decode_bytes(n_layers_sample, n_kv, 14, 2, 64, 4)
+    # prefill-1024 on the CPU, one timed pass (the reference computes every
+    # key, masked or not; the FLOP count below is still the causal one)
+    q = rng.standard_normal((1024, 14, 64), dtype=np.float32)
+    k = rng.standard_normal((1024, 2, 64), dtype=np.float32)
+    v = rng.standard_normal((1024, 2, 64), dtype=np.float32)
+    tp, _ = impl.time_attention([q], [k], [v], 0, 0.125, threads, warmup=0, reps=1)
+    return dict(value=nbytes / t / 1e9, unit="GB/s", cores=threads, kind=impl.kind,
+                sample="24 layers x decode n_kv=4096 (14 Q / 2 KV heads, head_dim 64, F32), "
+                       "median of 7 passes after 1 warmup; attn_qk -> softmax -> attn_kqv, "
+                       "barrier per node, static (head,row) split",
+                us_per_layer=t * 1e6 / n_layers_sample,
+                prefill1024_s=tp, prefill1024_tflops=causal_flops(1024, 14, 64) / tp / 1e12,
+                cpu=_cpu_model())
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary."""
+    p = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("bytes_per_launch")
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build runs "
+              "every kernel on a single MI355X and has no multi-GPU path.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import mi_hip_attn as mh
+    lib = mh.lib()
+    lib.init(0)
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    only = set(filter(None, args.only.split(",")))
+    want = lambda k: not only or k in only
+
+    res = {}
+    if want("decode"):
+        res["decode"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
+        print(f"# decode 24x4096: {res['decode']['gbps']:.1f} GB/s per step, kernel "
+              f"{res['decode']['kernel_gbps']:.1f} GB/s", file=sys.stderr, flush=True)
+    if want("prefill"):
+        res["prefill1024"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
+        res["prefill4096"] = bench_prefill(torch, mh, lib, stream, max(10, args.steps // 10),
+                                           max(2, args.warmup // 10), 4096)
+        print(f"# prefill 1024: {res['prefill1024']['tflops']:.2f} TF/s, 4096: "
+              f"{res['prefill4096']['tflops']:.2f} TF/s", file=sys.stderr, flush=True)
+    if want("d7b"):
+        res["decode7b"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup,
+                                       n_layers=1, n_kv=8192, h=28, hkv=4, d=128, f16=True)
+        print(f"# decode 7B F16 8192: {res['decode7b']['kernel_gbps']:.1f} GB/s", file=sys.stderr,
+              flush=True)
+    if want("perlayer"):
+        res["per_layer"] = bench_decode_per_layer(torch, mh, lib, stream, args.steps, args.warmup)
+        print(f"# per-layer launches: {res['per_layer']['us_per_layer']:.2f} us/layer",
+              file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.time()
+        cpu = cpu_baseline()
+        print(f"# cpu baseline {cpu['value']:.2f} GB/s ({time.time() - t0:.1f}s)", file=sys.stderr,
+              flush=True)
+
+    d = res.get("decode")
+    out = {
+        "metric": METRIC,
+        "value": round(d["gbps"], 2) if d else None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(d["ms_per_step"], 6) if d else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic N(0,1) Q/K/V generated on the device",
+        "config": {
+            "workload": "decode attention: 24 independent layer caches x n_kv=4096, 1 query "
+                        "token, 14 Q / 2 KV heads (GQA 7), head_dim 64, F32 K/V, one batched "
+                        "launch per step, cache sets rotated beyond the 256 MB MALL",
+            "n_layers": 24, "n_kv": 4096, "n_head": 14, "n_head_kv": 2, "head_dim": 64,
+            "cache_sets": d["sets"] if d else None,
+        },
+    }
+    if d:
+        out["roofline"] = {
+            "bound": "hbm", "achieved": round(d["kernel_gbps"], 2), "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s", "frac": round(d["kernel_gbps"] / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic(),
+            "bytes_per_launch": d["bytes"], "kernel_us": round(d["kernel_ms"] * 1e3, 3),
+        }
+    if cpu:
+        out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                               for k, v in cpu.items()}
+    if "prefill1024" in res:
+        p1, p4 = res["prefill1024"], res["prefill4096"]
+        out["prefill"] = {
+            "metric": "prefill-1024 causal attn TFLOP/s (14 Q / 2 KV heads, head_dim 64, F32)",
+            "tflops_1024": round(p1["tflops"], 2), "us_1024": round(p1["kernel_ms"] * 1e3, 2),
+            "tflops_4096": round(p4["tflops"], 2), "us_4096": round(p4["kernel_ms"] * 1e3, 2),
+            "roofline": {"bound": "mfma", "achieved": round(p1["tflops"], 2),
+                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(p1["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
+                         "flops_per_launch": p1["flops"]},
+        }
+    if "decode7b" in res:
+        r = res["decode7b"]
+        out["decode_7b_f16"] = {"n_kv": 8192, "gbps": round(r["kernel_gbps"], 1),
+                                "us": round(r["kernel_ms"] * 1e3, 2),
+                                "frac": round(r["kernel_gbps"] / HBM_PEAK_GBPS, 4)}
+    if "per_layer" in res:
+        out["decode_per_layer_launch"] = {k: round(v, 3) for k, v in res["per_layer"].items()}
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

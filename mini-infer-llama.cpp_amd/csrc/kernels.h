@@ -1,0 +1,43 @@
+// kernels.h -- host-side launchers of the HIP kernels (internal to the
+// library; the public surface is include/mi_hip_attn.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "attn_common.h"
+
+namespace mi {
+
+// decode.hip
+int decode_group_size(int n_rep);                       // G: Q heads per wave group
+size_t decode_record_floats(int head_dim, int group);   // floats per split partial
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
+                         hipStream_t stream);
+
+// prefill.hip
+size_t prefill_record_floats(int head_dim);             // floats per unit partial
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, hipStream_t stream);
+
+// nodes.hip -- node-level kernels on device tensors (byte strides).
+struct NodeView {
+  char* data;
+  int64_t ne[3];
+  int64_t nb[3];
+};
+hipError_t launch_attn_qk_node(const NodeView& dst, const NodeView& q, const NodeView& k,
+                               bool k_f16, int n_rep, hipStream_t stream);
+hipError_t launch_softmax_node(const NodeView& dst, const NodeView& src, int n_past, float scale,
+                               hipStream_t stream);
+hipError_t launch_attn_kqv_node(const NodeView& dst, const NodeView& probs, const NodeView& v,
+                                bool v_f16, int n_rep, hipStream_t stream);
+
+// Cache append: src F32 [head_dim, n_head_kv, n_tokens] (device, byte strides)
+// into dst rows [pos0, pos0 + n_tokens) of a [head_dim, n_head_kv, n_ctx]
+// cache with byte strides dst_s1 (head) and dst_s2 (position).
+hipError_t launch_kv_append(char* dst, int64_t dst_s1, int64_t dst_s2, bool dst_f16,
+                            const char* src, const int64_t src_nb[3], int head_dim,
+                            int n_head_kv, int pos0, int n_tokens, hipStream_t stream);
+
+}  // namespace mi

@@ -1,0 +1,1004 @@
+// runtime.hip -- host side of the C ABI declared in include/mi_hip_attn.h.
+//
+// Responsibilities: argument validation (every entry point returns a status
+// and never throws), device-allocation accounting, the device-resident KV
+// cache, launch planning for the decode and prefill kernels, the node-level
+// operators on device tensors, and the executor hook that lets the engine's
+// host graph route its attention nodes here.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <unordered_map>
+
+#include "attn_common.h"
+#include "kernels.h"
+#include "mi_hip_attn.h"
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Errors
+// ---------------------------------------------------------------------------
+thread_local char t_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(t_err, sizeof t_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(e == hipErrorOutOfMemory ? MI_HIP_E_NOMEM : MI_HIP_E_RUNTIME, "%s: %s", what,
+              hipGetErrorString(e));
+}
+
+#define MI_TRY_HIP(expr, what)            \
+  do {                                    \
+    hipError_t e_ = (expr);               \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Library state and device allocation accounting
+// ---------------------------------------------------------------------------
+struct State {
+  std::mutex mu;
+  int device = -1;
+  bool ready = false;
+  std::atomic<uint64_t> n_malloc{0}, n_free{0}, live{0}, peak{0};
+  std::atomic<uint64_t> limit{0};
+  // Shared split/merge workspace: [counters][partials]; zeroed on allocation,
+  // the kernels leave every counter at zero when they finish.
+  char* ws = nullptr;
+  size_t ws_bytes = 0;
+};
+State g;
+
+constexpr size_t kCounterBytes = 1 << 20;  // 256 Ki counters
+
+int dev_alloc(void** p, size_t bytes, const char* what) {
+  const uint64_t lim = g.limit.load();
+  if (lim && g.live.load() + bytes > lim)
+    return fail(MI_HIP_E_NOMEM, "%s: %zu bytes would exceed the allocation limit of %llu", what,
+                bytes, (unsigned long long)lim);
+  hipError_t e = hipMalloc(p, bytes);
+  if (e != hipSuccess) return hip_fail(e, what);
+  g.n_malloc++;
+  const uint64_t now = g.live.fetch_add(bytes) + bytes;
+  uint64_t pk = g.peak.load();
+  while (now > pk && !g.peak.compare_exchange_weak(pk, now)) {
+  }
+  return MI_HIP_OK;
+}
+
+void dev_free(void* p, size_t bytes) {
+  if (!p) return;
+  (void)hipFree(p);
+  g.n_free++;
+  g.live.fetch_sub(bytes);
+}
+
+int bind_device() {
+  if (!g.ready) return fail(MI_HIP_E_STATE, "mi_hip_init has not been called");
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur != g.device) MI_TRY_HIP(hipSetDevice(g.device), "hipSetDevice");
+  return MI_HIP_OK;
+}
+
+// Grows the workspace to at least `bytes` of partials. Growth synchronises the
+// device first, so no in-flight kernel still uses the old buffer.
+int ensure_workspace(size_t part_bytes) {
+  const size_t need = kCounterBytes + ((part_bytes + 255) & ~size_t(255));
+  std::lock_guard<std::mutex> lk(g.mu);
+  if (g.ws && g.ws_bytes >= need) return MI_HIP_OK;
+  if (g.ws) {
+    MI_TRY_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    dev_free(g.ws, g.ws_bytes);
+    g.ws = nullptr;
+    g.ws_bytes = 0;
+  }
+  void* p = nullptr;
+  int rc = dev_alloc(&p, need, "workspace");
+  if (rc) return rc;
+  hipError_t e = hipMemset(p, 0, need);
+  if (e != hipSuccess) {
+    dev_free(p, need);
+    return hip_fail(e, "hipMemset(workspace)");
+  }
+  g.ws = static_cast<char*>(p);
+  g.ws_bytes = need;
+  return MI_HIP_OK;
+}
+
+unsigned* ws_counters() { return reinterpret_cast<unsigned*>(g.ws); }
+float* ws_part() { return reinterpret_cast<float*>(g.ws + kCounterBytes); }
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+
+// ---------------------------------------------------------------------------
+// Launch planning
+// ---------------------------------------------------------------------------
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodePlan {
+  int group = 1, n_chunks = 1, splits = 1;
+  size_t part_floats = 0, counters = 0;
+};
+
+// Splits per (item, head chunk) so the launch has about `target` workgroups,
+// at most one 64-position tile per split.
+DecodePlan plan_decode(int n_items, int n_head_kv, int n_rep, int head_dim, int max_n_kv) {
+  DecodePlan p;
+  p.group = mi::decode_group_size(n_rep);
+  p.n_chunks = n_rep / p.group;
+  const int groups = n_items * n_head_kv * p.n_chunks;
+  const int target = std::max(1, env_int("MI_HIP_DECODE_WGS", 1024));
+  const int max_splits = std::max(1, (max_n_kv + mi::kDecodeTile - 1) / mi::kDecodeTile);
+  int s = (target + groups - 1) / groups;
+  const int forced = env_int("MI_HIP_DECODE_SPLITS", 0);
+  if (forced > 0) s = forced;
+  p.splits = std::max(1, std::min(s, max_splits));
+  p.counters = (size_t)groups;
+  p.part_floats = p.splits > 1 ? (size_t)groups * p.splits * mi::decode_record_floats(head_dim, p.group) : 0;
+  return p;
+}
+
+struct PrefillPlan {
+  int chunk = 1, n_qblocks = 1, units_per_head = 1, n_units = 1;
+  size_t part_floats = 0, counters = 0;
+};
+
+PrefillPlan plan_prefill(int n_head, int head_dim, int n_past, int n_tokens) {
+  PrefillPlan p;
+  const int kt_all = (n_past + n_tokens + 31) / 32;
+  const int c0 = (n_past + 31) / 32;
+  p.n_qblocks = (n_tokens + 31) / 32;
+  const int last = p.n_qblocks - 1;
+  const int kt_last = std::min(c0 + last + 1, kt_all);
+  // key tiles over all query blocks of one head
+  const int64_t tiles = (int64_t)(c0 + 1 + c0 + last) * last / 2 + kt_last;
+  const int target = std::max(1, env_int("MI_HIP_PREFILL_UNITS", 2048));
+  int64_t c = (tiles * n_head + target - 1) / target;
+  const int forced = env_int("MI_HIP_PREFILL_CHUNK", 0);
+  if (forced > 0) c = forced;
+  p.chunk = (int)std::max<int64_t>(1, std::min<int64_t>(c, kt_all));
+  p.units_per_head = (int)(mi::ceil_prefix(c0 + last, p.chunk) - mi::ceil_prefix(c0, p.chunk) +
+                           (kt_last + p.chunk - 1) / p.chunk);
+  p.n_units = p.units_per_head * n_head;
+  p.counters = (size_t)n_head * p.n_qblocks;
+  p.part_floats = (size_t)p.n_units * mi::prefill_record_floats(head_dim);
+  return p;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// KV cache object
+// ---------------------------------------------------------------------------
+struct mi_hip_kv {
+  mi_hip_kv_desc d;
+  char* base = nullptr;
+  size_t bytes = 0;
+  size_t tensor_bytes = 0;  // one layer's K (or V)
+  int64_t s1 = 0, s2 = 0;   // byte strides: head, position
+  int elt = 4;
+  float* stage = nullptr;   // host-node staging: Q, O, appended rows
+  size_t stage_bytes = 0;
+  size_t q_floats = 0, row_floats = 0;
+  hipStream_t stream = nullptr;
+
+  char* tensor(int layer, int which) const {
+    return base + (size_t)(2 * layer + which) * tensor_bytes;
+  }
+};
+
+namespace {
+
+struct Resolved {
+  const char* k;
+  const char* v;
+  int64_t k_s1, k_s2, v_s1, v_s2;
+  bool f16;
+  int head_dim, n_head_kv;
+  int n_ctx;  // -1 when unknown (explicit tensors)
+};
+
+int resolve_kv(const mi_hip_attn_args* a, Resolved* r) {
+  if (a->kv) {
+    const mi_hip_kv* kv = a->kv;
+    if (a->layer < 0 || a->layer >= kv->d.n_layer)
+      return fail(MI_HIP_E_INVALID, "layer %d out of range [0, %d)", a->layer, kv->d.n_layer);
+    r->k = kv->tensor(a->layer, 0);
+    r->v = kv->tensor(a->layer, 1);
+    r->k_s1 = r->v_s1 = kv->s1;
+    r->k_s2 = r->v_s2 = kv->s2;
+    r->f16 = kv->d.type == MI_TYPE_F16;
+    r->head_dim = kv->d.head_dim;
+    r->n_head_kv = kv->d.n_head_kv;
+    r->n_ctx = kv->d.n_ctx;
+    return MI_HIP_OK;
+  }
+  if (!a->k || !a->v) return fail(MI_HIP_E_INVALID, "no KV source: kv and k/v are NULL");
+  if (a->kv_type != MI_TYPE_F32 && a->kv_type != MI_TYPE_F16)
+    return fail(MI_HIP_E_UNSUPPORTED, "K/V type %d: only F32 (0) and F16 (1)", a->kv_type);
+  const int elt = a->kv_type == MI_TYPE_F16 ? 2 : 4;
+  if (a->k_nb[0] != (size_t)elt || a->v_nb[0] != (size_t)elt)
+    return fail(MI_HIP_E_UNSUPPORTED, "K/V nb[0] must be the element size (%d)", elt);
+  const size_t al = (size_t)elt * 4;
+  for (int i = 1; i < 3; ++i)
+    if (a->k_nb[i] % al || a->v_nb[i] % al)
+      return fail(MI_HIP_E_UNSUPPORTED, "K/V nb[1], nb[2] must be multiples of %zu bytes", al);
+  if (!aligned(a->k, al) || !aligned(a->v, al))
+    return fail(MI_HIP_E_UNSUPPORTED, "K/V data must be %zu-byte aligned", al);
+  r->k = static_cast<const char*>(a->k);
+  r->v = static_cast<const char*>(a->v);
+  r->k_s1 = (int64_t)a->k_nb[1];
+  r->k_s2 = (int64_t)a->k_nb[2];
+  r->v_s1 = (int64_t)a->v_nb[1];
+  r->v_s2 = (int64_t)a->v_nb[2];
+  r->f16 = a->kv_type == MI_TYPE_F16;
+  r->head_dim = a->head_dim;
+  r->n_head_kv = a->n_head_kv;
+  r->n_ctx = -1;
+  return MI_HIP_OK;
+}
+
+// Checks everything the fused kernels assume about one problem.
+int check_problem(const mi_hip_attn_args* a, const Resolved& r) {
+  if (r.head_dim != 64 && r.head_dim != 128)
+    return fail(MI_HIP_E_UNSUPPORTED, "head_dim %d: the kernels cover 64 and 128", r.head_dim);
+  if (r.n_head_kv <= 0) return fail(MI_HIP_E_INVALID, "n_head_kv must be positive");
+  if (a->n_rep <= 0 || a->n_head <= 0)
+    return fail(MI_HIP_E_INVALID, "n_head (%d) and n_rep (%d) must be positive", a->n_head, a->n_rep);
+  if (a->n_head != a->n_rep * r.n_head_kv)
+    return fail(MI_HIP_E_INVALID, "n_head (%d) must equal n_rep (%d) * n_head_kv (%d)", a->n_head,
+                a->n_rep, r.n_head_kv);
+  if (a->n_past < 0 || a->n_tokens < 1)
+    return fail(MI_HIP_E_INVALID, "n_past (%d) must be >= 0 and n_tokens (%d) >= 1", a->n_past,
+                a->n_tokens);
+  if (r.n_ctx >= 0 && (int64_t)a->n_past + a->n_tokens > r.n_ctx)
+    return fail(MI_HIP_E_INVALID, "n_past + n_tokens (%d) exceeds n_ctx (%d)",
+                a->n_past + a->n_tokens, r.n_ctx);
+  if (!std::isfinite(a->scale)) return fail(MI_HIP_E_INVALID, "scale must be finite");
+  if (!a->q || !a->out) return fail(MI_HIP_E_INVALID, "q and out must be device pointers");
+  if (a->q_nb[0] != 4 || a->out_nb[0] != 4)
+    return fail(MI_HIP_E_UNSUPPORTED, "q/out nb[0] must be 4 (head_dim contiguous)");
+  for (int i = 1; i < 3; ++i)
+    if (a->q_nb[i] % 16 || a->out_nb[i] % 16)
+      return fail(MI_HIP_E_UNSUPPORTED, "q/out nb[1], nb[2] must be multiples of 16 bytes");
+  if (!aligned(a->q, 16) || !aligned(a->out, 16))
+    return fail(MI_HIP_E_UNSUPPORTED, "q/out must be 16-byte aligned");
+  return MI_HIP_OK;
+}
+
+mi::DecodeItem make_item(const mi_hip_attn_args* a, const Resolved& r) {
+  mi::DecodeItem it{};
+  it.k = r.k;
+  it.v = r.v;
+  it.q = a->q;
+  it.out = a->out;
+  it.k_s1 = r.k_s1;
+  it.k_s2 = r.k_s2;
+  it.v_s1 = r.v_s1;
+  it.v_s2 = r.v_s2;
+  it.q_s1 = (int64_t)a->q_nb[1];
+  it.o_s1 = (int64_t)a->out_nb[1];
+  it.n_kv = a->n_past + 1;
+  return it;
+}
+
+int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
+  Resolved r0;
+  int rc = resolve_kv(&items[0], &r0);
+  if (rc) return rc;
+  int max_n_kv = 0;
+  for (int i = 0; i < n; ++i) max_n_kv = std::max(max_n_kv, items[i].n_past + 1);
+  const int chunk_items = std::min(n, mi::kDecodeMaxItems);
+  const DecodePlan plan =
+      plan_decode(chunk_items, r0.n_head_kv, items[0].n_rep, r0.head_dim, max_n_kv);
+  if (plan.counters * sizeof(unsigned) > kCounterBytes)
+    return fail(MI_HIP_E_UNSUPPORTED, "too many head groups in one launch");
+  rc = ensure_workspace(plan.part_floats * sizeof(float));
+  if (rc) return rc;
+  for (int base = 0; base < n; base += mi::kDecodeMaxItems) {
+    const int cnt = std::min(mi::kDecodeMaxItems, n - base);
+    mi::DecodeParams p{};
+    for (int i = 0; i < cnt; ++i) {
+      Resolved r;
+      rc = resolve_kv(&items[base + i], &r);
+      if (rc) return rc;
+      p.item[i] = make_item(&items[base + i], r);
+    }
+    p.n_items = cnt;
+    p.n_rep = items[0].n_rep;
+    p.n_head_kv = r0.n_head_kv;
+    p.n_chunks = plan.n_chunks;
+    p.splits = plan.splits;
+    p.scale_log2e = items[0].scale * kLog2e;
+    p.part = ws_part();
+    p.counter = ws_counters();
+    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, stream);
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+  }
+  return MI_HIP_OK;
+}
+
+int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream) {
+  const PrefillPlan plan = plan_prefill(a->n_head, r.head_dim, a->n_past, a->n_tokens);
+  if (plan.counters * sizeof(unsigned) > kCounterBytes)
+    return fail(MI_HIP_E_UNSUPPORTED, "too many query blocks in one launch");
+  int rc = ensure_workspace(plan.part_floats * sizeof(float));
+  if (rc) return rc;
+  mi::PrefillParams p{};
+  p.k = r.k;
+  p.v = r.v;
+  p.q = a->q;
+  p.out = a->out;
+  p.k_s1 = r.k_s1;
+  p.k_s2 = r.k_s2;
+  p.v_s1 = r.v_s1;
+  p.v_s2 = r.v_s2;
+  p.q_s1 = (int64_t)a->q_nb[1];
+  p.q_s2 = (int64_t)a->q_nb[2];
+  p.o_s1 = (int64_t)a->out_nb[1];
+  p.o_s2 = (int64_t)a->out_nb[2];
+  p.n_head = a->n_head;
+  p.n_rep = a->n_rep;
+  p.n_past = a->n_past;
+  p.n_tokens = a->n_tokens;
+  p.chunk_tiles = plan.chunk;
+  p.n_qblocks = plan.n_qblocks;
+  p.units_per_head = plan.units_per_head;
+  p.n_units = plan.n_units;
+  p.scale_log2e = a->scale * kLog2e;
+  p.part = ws_part();
+  p.counter = ws_counters();
+  hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, stream);
+  if (e != hipSuccess) return hip_fail(e, "prefill launch");
+  return MI_HIP_OK;
+}
+
+// Workspace bytes that cover every decode and prefill call up to n_ctx.
+size_t workspace_for(const mi_hip_kv_desc& d) {
+  const int n_rep = d.n_head / d.n_head_kv;
+  const DecodePlan dp = plan_decode(1, d.n_head_kv, n_rep, d.head_dim, d.n_ctx);
+  size_t need = dp.part_floats;
+  for (int t : {d.n_ctx, std::max(2, d.n_ctx / 2)}) {
+    const PrefillPlan pp = plan_prefill(d.n_head, d.head_dim, 0, t);
+    need = std::max(need, pp.part_floats);
+  }
+  return need * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// Executor hook tables (no allocation per step)
+// ---------------------------------------------------------------------------
+struct Binding {
+  mi_hip_kv* kv;
+  int layer;
+  int which;
+};
+std::mutex g_bind_mu;
+std::unordered_map<const mi_tensor*, Binding> g_bind;
+
+const Binding* find_binding(const mi_tensor* t) {
+  if (!t) return nullptr;
+  std::lock_guard<std::mutex> lk(g_bind_mu);
+  auto it = g_bind.find(t);
+  return it == g_bind.end() ? nullptr : &it->second;
+}
+
+// Fixed-capacity pointer map, cleared in O(1) by bumping a generation.
+template <int N>
+struct PtrMap {
+  struct Slot {
+    const void* key;
+    uint32_t gen;
+    int32_t val;
+  };
+  Slot slot[N];
+  uint32_t gen = 1;
+  void clear() { ++gen; }
+  static uint32_t hash(const void* p) {
+    uint64_t x = reinterpret_cast<uintptr_t>(p);
+    x ^= x >> 33;
+    x *= 0xff51afd7ed558ccdULL;
+    x ^= x >> 33;
+    return (uint32_t)x;
+  }
+  int32_t* find(const void* key, bool insert) {
+    uint32_t h = hash(key) & (N - 1);
+    for (int probe = 0; probe < N; ++probe, h = (h + 1) & (N - 1)) {
+      Slot& s = slot[h];
+      if (s.gen != gen) {
+        if (!insert) return nullptr;
+        s.key = key;
+        s.gen = gen;
+        s.val = 0;
+        return &s.val;
+      }
+      if (s.key == key) return &s.val;
+    }
+    return nullptr;
+  }
+};
+
+enum Role : int32_t { kNone = 0, kFusedQK = 1, kFusedSoftmax = 2, kFusedKQV = 3 };
+
+std::mutex g_plan_mu;
+PtrMap<1 << 15> g_readers;  // ATTN_QK / SOFTMAX node -> number of readers
+PtrMap<1 << 15> g_roles;    // node -> Role
+
+int32_t role_of(const mi_tensor* t) {
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  int32_t* r = g_roles.find(t, false);
+  return r ? *r : kNone;
+}
+
+bool contiguous3(const mi_tensor* t) {
+  return t->nb[0] == 4 && t->nb[1] == 4 * (size_t)t->ne[0] &&
+         t->nb[2] == t->nb[1] * (size_t)t->ne[1];
+}
+
+mi::NodeView view_of(const mi_tensor* t) {
+  mi::NodeView v;
+  v.data = static_cast<char*>(t->data);
+  for (int i = 0; i < 3; ++i) {
+    v.ne[i] = t->ne[i];
+    v.nb[i] = (int64_t)t->nb[i];
+  }
+  return v;
+}
+
+int check_kv_tensor(const mi_tensor* t, const char* what) {
+  if (!t || !t->data) return fail(MI_HIP_E_INVALID, "%s: missing tensor or data", what);
+  if (t->type != MI_TYPE_F32 && t->type != MI_TYPE_F16)
+    return fail(MI_HIP_E_UNSUPPORTED, "%s: type %d (F32 or F16 only)", what, (int)t->type);
+  if (t->nb[0] != (t->type == MI_TYPE_F16 ? 2u : 4u))
+    return fail(MI_HIP_E_UNSUPPORTED, "%s: nb[0] must be the element size", what);
+  return MI_HIP_OK;
+}
+
+int check_f32(const mi_tensor* t, const char* what) {
+  if (!t || !t->data) return fail(MI_HIP_E_INVALID, "%s: missing tensor or data", what);
+  if (t->type != MI_TYPE_F32) return fail(MI_HIP_E_UNSUPPORTED, "%s: must be F32", what);
+  return MI_HIP_OK;
+}
+
+// Fills args for the fused chain ending at ATTN_KQV node `kqv`, all tensors
+// device-resident.
+int fused_args_from_nodes(mi_tensor* kqv, mi_hip_attn_args* a) {
+  if (!kqv || kqv->op != MI_OP_ATTN_KQV) return fail(MI_HIP_E_INVALID, "dst is not an ATTN_KQV node");
+  const mi_tensor* sm = kqv->src[0];
+  if (!sm || sm->op != MI_OP_SOFTMAX) return fail(MI_HIP_E_INVALID, "ATTN_KQV src[0] is not SOFTMAX");
+  const mi_tensor* qk = sm->src[0];
+  if (!qk || qk->op != MI_OP_ATTN_QK) return fail(MI_HIP_E_INVALID, "SOFTMAX src[0] is not ATTN_QK");
+  const mi_tensor* q = qk->src[0];
+  const mi_tensor* k = qk->src[1];
+  const mi_tensor* v = kqv->src[1];
+  int rc;
+  if ((rc = check_f32(q, "Q")) || (rc = check_kv_tensor(k, "K")) || (rc = check_kv_tensor(v, "V")) ||
+      (rc = check_f32(kqv, "out")))
+    return rc;
+  if (k->type != v->type) return fail(MI_HIP_E_UNSUPPORTED, "K and V types differ");
+  const int n_past = mi_tensor_param_i32(qk, 0);
+  const int n_rep = mi_tensor_param_i32(qk, 1);
+  if (mi_tensor_param_i32(sm, 0) != n_past)
+    return fail(MI_HIP_E_INVALID, "SOFTMAX n_past differs from ATTN_QK n_past");
+  if (mi_tensor_param_i32(kqv, 0) != n_rep)
+    return fail(MI_HIP_E_INVALID, "ATTN_KQV n_rep differs from ATTN_QK n_rep");
+  if (qk->ne[0] != (int64_t)n_past + q->ne[2] || qk->ne[1] != q->ne[2] || qk->ne[2] != q->ne[1])
+    return fail(MI_HIP_E_INVALID, "ATTN_QK shape is not [n_past+n_tokens, n_tokens, n_head]");
+  if (kqv->ne[0] != q->ne[0] || kqv->ne[1] != q->ne[1] || kqv->ne[2] != q->ne[2])
+    return fail(MI_HIP_E_INVALID, "ATTN_KQV shape is not [head_dim, n_head, n_tokens]");
+  if (k->ne[0] != q->ne[0] || v->ne[0] != q->ne[0] || k->ne[1] != v->ne[1])
+    return fail(MI_HIP_E_INVALID, "K/V head_dim or n_head_kv mismatch");
+  if (k->ne[2] < qk->ne[0] || v->ne[2] < qk->ne[0])
+    return fail(MI_HIP_E_INVALID, "K/V hold fewer than n_past + n_tokens positions");
+  std::memset(a, 0, sizeof *a);
+  a->k = k->data;
+  a->v = v->data;
+  for (int i = 0; i < 3; ++i) {
+    a->k_nb[i] = k->nb[i];
+    a->v_nb[i] = v->nb[i];
+    a->q_nb[i] = q->nb[i];
+    a->out_nb[i] = kqv->nb[i];
+  }
+  a->kv_type = k->type;
+  a->head_dim = (int32_t)q->ne[0];
+  a->n_head_kv = (int32_t)k->ne[1];
+  a->q = static_cast<const float*>(q->data);
+  a->out = static_cast<float*>(kqv->data);
+  a->n_head = (int32_t)q->ne[1];
+  a->n_rep = n_rep;
+  a->n_past = n_past;
+  a->n_tokens = (int32_t)q->ne[2];
+  a->scale = mi_tensor_param_f32(sm, 1);
+  return MI_HIP_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+int mi_hip_init(int device) {
+  std::lock_guard<std::mutex> lk(g.mu);
+  if (g.ready) {
+    if (device == g.device) return MI_HIP_OK;
+    return fail(MI_HIP_E_STATE, "already initialised on device %d", g.device);
+  }
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0)
+    return fail(MI_HIP_E_NODEVICE, "no HIP device is visible");
+  if (device < 0 || device >= n)
+    return fail(MI_HIP_E_INVALID, "device %d out of range [0, %d)", device, n);
+  hipDeviceProp_t prop;
+  MI_TRY_HIP(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(MI_HIP_E_NODEVICE, "device %d is %s; this library is built for gfx950 only", device,
+                prop.gcnArchName);
+  MI_TRY_HIP(hipSetDevice(device), "hipSetDevice");
+  g.device = device;
+  g.ready = true;
+  t_err[0] = '\0';
+  return MI_HIP_OK;
+}
+
+int mi_hip_shutdown(void) {
+  if (!g.ready) return MI_HIP_OK;
+  int rc = bind_device();
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g.mu);
+  (void)hipDeviceSynchronize();
+  dev_free(g.ws, g.ws_bytes);
+  g.ws = nullptr;
+  g.ws_bytes = 0;
+  g.ready = false;
+  g.device = -1;
+  return MI_HIP_OK;
+}
+
+const char* mi_hip_last_error(void) { return t_err; }
+
+int mi_hip_abi_layout(size_t* out, int n) {
+  if (!out || n < 15) return fail(MI_HIP_E_INVALID, "need an array of at least 15 entries");
+  out[0] = sizeof(mi_tensor);
+  out[1] = offsetof(mi_tensor, type);
+  out[2] = offsetof(mi_tensor, ne);
+  out[3] = offsetof(mi_tensor, nb);
+  out[4] = offsetof(mi_tensor, op);
+  out[5] = offsetof(mi_tensor, op_params);
+  out[6] = offsetof(mi_tensor, src);
+  out[7] = offsetof(mi_tensor, data);
+  out[8] = offsetof(mi_tensor, view_src);
+  out[9] = offsetof(mi_tensor, view_offs);
+  out[10] = offsetof(mi_tensor, n_children);
+  out[11] = offsetof(mi_tensor, flags);
+  out[12] = offsetof(mi_tensor, name);
+  out[13] = offsetof(mi_tensor, extra);
+  out[14] = sizeof(mi_cgraph);
+  return MI_HIP_OK;
+}
+
+int mi_hip_get_alloc_stats(mi_hip_alloc_stats* out) {
+  if (!out) return fail(MI_HIP_E_INVALID, "out is NULL");
+  out->n_malloc = g.n_malloc.load();
+  out->n_free = g.n_free.load();
+  out->bytes_live = g.live.load();
+  out->bytes_peak = g.peak.load();
+  return MI_HIP_OK;
+}
+
+int mi_hip_set_alloc_limit(uint64_t bytes) {
+  g.limit.store(bytes);
+  return MI_HIP_OK;
+}
+
+int mi_hip_kv_create(const mi_hip_kv_desc* d, mi_hip_kv** out) {
+  if (!d || !out) return fail(MI_HIP_E_INVALID, "desc and out must be non-NULL");
+  *out = nullptr;
+  if (d->n_layer <= 0 || d->n_ctx <= 0 || d->n_head_kv <= 0 || d->n_head <= 0)
+    return fail(MI_HIP_E_INVALID, "n_layer, n_ctx, n_head_kv and n_head must be positive");
+  if (d->n_head % d->n_head_kv != 0)
+    return fail(MI_HIP_E_INVALID, "n_head (%d) must be a multiple of n_head_kv (%d)", d->n_head,
+                d->n_head_kv);
+  if (d->head_dim != 64 && d->head_dim != 128)
+    return fail(MI_HIP_E_UNSUPPORTED, "head_dim %d: the kernels cover 64 and 128", d->head_dim);
+  if (d->type != MI_TYPE_F32 && d->type != MI_TYPE_F16)
+    return fail(MI_HIP_E_UNSUPPORTED, "cache type %d: F32 (0) or F16 (1)", d->type);
+  int rc = bind_device();
+  if (rc) return rc;
+
+  mi_hip_kv* kv = new (std::nothrow) mi_hip_kv();
+  if (!kv) return fail(MI_HIP_E_NOMEM, "host allocation failed");
+  kv->d = *d;
+  kv->elt = d->type == MI_TYPE_F16 ? 2 : 4;
+  kv->s1 = (int64_t)d->head_dim * kv->elt;
+  kv->s2 = kv->s1 * d->n_head_kv;
+  kv->tensor_bytes = (size_t)kv->s2 * d->n_ctx;
+  kv->bytes = kv->tensor_bytes * 2 * d->n_layer;
+  kv->q_floats = (size_t)d->n_ctx * d->n_head * d->head_dim;
+  kv->row_floats = (size_t)d->n_ctx * d->n_head_kv * d->head_dim;
+  kv->stage_bytes = (2 * kv->q_floats + kv->row_floats) * sizeof(float);
+
+  void* p = nullptr;
+  if ((rc = dev_alloc(&p, kv->bytes, "KV cache"))) {
+    delete kv;
+    return rc;
+  }
+  kv->base = static_cast<char*>(p);
+  if ((rc = dev_alloc(&p, kv->stage_bytes, "KV staging"))) {
+    dev_free(kv->base, kv->bytes);
+    delete kv;
+    return rc;
+  }
+  kv->stage = static_cast<float*>(p);
+  hipError_t e = hipMemset(kv->base, 0, kv->bytes);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    dev_free(kv->stage, kv->stage_bytes);
+    dev_free(kv->base, kv->bytes);
+    delete kv;
+    return hip_fail(e, "KV cache init");
+  }
+  if ((rc = ensure_workspace(workspace_for(*d)))) {
+    (void)hipStreamDestroy(kv->stream);
+    dev_free(kv->stage, kv->stage_bytes);
+    dev_free(kv->base, kv->bytes);
+    delete kv;
+    return rc;
+  }
+  *out = kv;
+  return MI_HIP_OK;
+}
+
+int mi_hip_kv_destroy(mi_hip_kv* kv) {
+  if (!kv) return MI_HIP_OK;
+  int rc = bind_device();
+  if (rc) return rc;
+  {
+    std::lock_guard<std::mutex> lk(g_bind_mu);
+    for (auto it = g_bind.begin(); it != g_bind.end();)
+      it = it->second.kv == kv ? g_bind.erase(it) : std::next(it);
+  }
+  (void)hipStreamSynchronize(kv->stream);
+  (void)hipStreamDestroy(kv->stream);
+  dev_free(kv->stage, kv->stage_bytes);
+  dev_free(kv->base, kv->bytes);
+  delete kv;
+  return MI_HIP_OK;
+}
+
+int mi_hip_kv_view(mi_hip_kv* kv, int layer, int which, void** data, int64_t ne[4], size_t nb[4]) {
+  if (!kv || !data) return fail(MI_HIP_E_INVALID, "kv and data must be non-NULL");
+  if (layer < 0 || layer >= kv->d.n_layer || (which != 0 && which != 1))
+    return fail(MI_HIP_E_INVALID, "layer %d / which %d out of range", layer, which);
+  *data = kv->tensor(layer, which);
+  if (ne) {
+    ne[0] = kv->d.head_dim;
+    ne[1] = kv->d.n_head_kv;
+    ne[2] = kv->d.n_ctx;
+    ne[3] = 1;
+  }
+  if (nb) {
+    nb[0] = (size_t)kv->elt;
+    nb[1] = (size_t)kv->s1;
+    nb[2] = (size_t)kv->s2;
+    nb[3] = (size_t)kv->s2 * kv->d.n_ctx;
+  }
+  return MI_HIP_OK;
+}
+
+int mi_hip_kv_write(mi_hip_kv* kv, int layer, int which, int pos0, int n_tokens, const float* src,
+                    const size_t src_nb[3], int src_on_device, void* stream) {
+  if (!kv || !src || !src_nb) return fail(MI_HIP_E_INVALID, "kv, src and src_nb must be non-NULL");
+  if (layer < 0 || layer >= kv->d.n_layer || (which != 0 && which != 1))
+    return fail(MI_HIP_E_INVALID, "layer %d / which %d out of range", layer, which);
+  if (pos0 < 0 || n_tokens < 0 || (int64_t)pos0 + n_tokens > kv->d.n_ctx)
+    return fail(MI_HIP_E_INVALID, "positions [%d, %d) outside [0, %d)", pos0, pos0 + n_tokens,
+                kv->d.n_ctx);
+  if (src_nb[0] % 4 || src_nb[1] % 4 || src_nb[2] % 4)
+    return fail(MI_HIP_E_INVALID, "src strides must be multiples of 4 bytes");
+  if (n_tokens == 0) return MI_HIP_OK;
+  int rc = bind_device();
+  if (rc) return rc;
+  hipStream_t st = stream ? static_cast<hipStream_t>(stream) : nullptr;
+  char* dst = kv->tensor(layer, which);
+  const int D = kv->d.head_dim, H = kv->d.n_head_kv;
+  const bool src_contig = src_nb[0] == 4 && src_nb[1] == 4u * D && src_nb[2] == 4u * D * H;
+  const char* dev_src = reinterpret_cast<const char*>(src);
+  int64_t nb[3] = {(int64_t)src_nb[0], (int64_t)src_nb[1], (int64_t)src_nb[2]};
+  if (!src_on_device) {
+    // Host rows: one contiguous copy straight into an F32 cache, else via staging.
+    const size_t bytes = (size_t)n_tokens * D * H * sizeof(float);
+    if (src_contig && kv->elt == 4) {
+      MI_TRY_HIP(hipMemcpyAsync(dst + (size_t)pos0 * kv->s2, src, bytes, hipMemcpyHostToDevice, st),
+                 "hipMemcpyAsync(K/V rows)");
+      MI_TRY_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+      return MI_HIP_OK;
+    }
+    if (!src_contig) return fail(MI_HIP_E_UNSUPPORTED, "host K/V rows must be contiguous");
+    float* stage_rows = kv->stage + 2 * kv->q_floats;
+    MI_TRY_HIP(hipMemcpyAsync(stage_rows, src, bytes, hipMemcpyHostToDevice, st),
+               "hipMemcpyAsync(K/V rows)");
+    dev_src = reinterpret_cast<const char*>(stage_rows);
+    nb[0] = 4;
+    nb[1] = 4LL * D;
+    nb[2] = 4LL * D * H;
+  }
+  hipError_t e = mi::launch_kv_append(dst, kv->s1, kv->s2, kv->elt == 2, dev_src, nb, D, H, pos0,
+                                      n_tokens, st);
+  if (e != hipSuccess) return hip_fail(e, "kv append launch");
+  if (!src_on_device) MI_TRY_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  return MI_HIP_OK;
+}
+
+int mi_hip_kv_bind(mi_hip_kv* kv, int layer, int which, const mi_tensor* host_kv) {
+  if (!kv || !host_kv) return fail(MI_HIP_E_INVALID, "kv and host_kv must be non-NULL");
+  if (layer < 0 || layer >= kv->d.n_layer || (which != 0 && which != 1))
+    return fail(MI_HIP_E_INVALID, "layer %d / which %d out of range", layer, which);
+  if (host_kv->ne[0] != kv->d.head_dim || host_kv->ne[1] != kv->d.n_head_kv ||
+      host_kv->ne[2] > kv->d.n_ctx)
+    return fail(MI_HIP_E_INVALID, "host tensor shape does not match the cache");
+  std::lock_guard<std::mutex> lk(g_bind_mu);
+  g_bind[host_kv] = Binding{kv, layer, which};
+  return MI_HIP_OK;
+}
+
+int mi_hip_attn_fwd(const mi_hip_attn_args* a) {
+  if (!a) return fail(MI_HIP_E_INVALID, "args is NULL");
+  Resolved r;
+  int rc = resolve_kv(a, &r);
+  if (rc) return rc;
+  if ((rc = check_problem(a, r))) return rc;
+  if ((rc = bind_device())) return rc;
+  hipStream_t st = static_cast<hipStream_t>(a->stream);
+  return a->n_tokens == 1 ? run_decode(a, 1, st) : run_prefill(a, r, st);
+}
+
+int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* stream) {
+  if (!items || n_items <= 0) return fail(MI_HIP_E_INVALID, "need at least one item");
+  Resolved r0;
+  int rc = resolve_kv(&items[0], &r0);
+  if (rc) return rc;
+  for (int i = 0; i < n_items; ++i) {
+    Resolved r;
+    if ((rc = resolve_kv(&items[i], &r))) return rc;
+    if ((rc = check_problem(&items[i], r))) return rc;
+    if (items[i].n_tokens != 1) return fail(MI_HIP_E_INVALID, "item %d: n_tokens must be 1", i);
+    if (r.head_dim != r0.head_dim || r.f16 != r0.f16 || r.n_head_kv != r0.n_head_kv ||
+        items[i].n_rep != items[0].n_rep || items[i].scale != items[0].scale)
+      return fail(MI_HIP_E_INVALID, "item %d: shape, type or scale differs from item 0", i);
+  }
+  if ((rc = bind_device())) return rc;
+  return run_decode(items, n_items, static_cast<hipStream_t>(stream));
+}
+
+int mi_hip_op_attn_qk(mi_tensor* dst, void* stream) {
+  if (!dst || dst->op != MI_OP_ATTN_QK) return fail(MI_HIP_E_INVALID, "dst is not an ATTN_QK node");
+  const mi_tensor* q = dst->src[0];
+  const mi_tensor* k = dst->src[1];
+  int rc;
+  if ((rc = check_f32(dst, "scores")) || (rc = check_f32(q, "Q")) || (rc = check_kv_tensor(k, "K")))
+    return rc;
+  const int n_rep = mi_tensor_param_i32(dst, 1);
+  if (n_rep <= 0) return fail(MI_HIP_E_INVALID, "n_rep must be positive");
+  if (dst->ne[1] != q->ne[2] || dst->ne[2] != q->ne[1] || k->ne[0] != q->ne[0])
+    return fail(MI_HIP_E_INVALID, "ATTN_QK shapes are inconsistent");
+  if ((q->ne[1] - 1) / n_rep >= k->ne[1] || dst->ne[0] > k->ne[2])
+    return fail(MI_HIP_E_INVALID, "ATTN_QK reads outside the K tensor");
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_attn_qk_node(view_of(dst), view_of(q), view_of(k),
+                                         k->type == MI_TYPE_F16, n_rep,
+                                         static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "attn_qk launch");
+}
+
+int mi_hip_op_softmax(mi_tensor* dst, void* stream) {
+  if (!dst || dst->op != MI_OP_SOFTMAX) return fail(MI_HIP_E_INVALID, "dst is not a SOFTMAX node");
+  const mi_tensor* s = dst->src[0];
+  int rc;
+  if ((rc = check_f32(dst, "probs")) || (rc = check_f32(s, "scores"))) return rc;
+  for (int i = 0; i < 3; ++i)
+    if (dst->ne[i] != s->ne[i]) return fail(MI_HIP_E_INVALID, "SOFTMAX shape differs from its source");
+  const int n_past = mi_tensor_param_i32(dst, 0);
+  if (n_past < 0) return fail(MI_HIP_E_INVALID, "n_past must be >= 0");
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_softmax_node(view_of(dst), view_of(s), n_past,
+                                         mi_tensor_param_f32(dst, 1), static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "softmax launch");
+}
+
+int mi_hip_op_attn_kqv(mi_tensor* dst, void* stream) {
+  if (!dst || dst->op != MI_OP_ATTN_KQV) return fail(MI_HIP_E_INVALID, "dst is not an ATTN_KQV node");
+  const mi_tensor* pr = dst->src[0];
+  const mi_tensor* v = dst->src[1];
+  int rc;
+  if ((rc = check_f32(dst, "out")) || (rc = check_f32(pr, "probs")) || (rc = check_kv_tensor(v, "V")))
+    return rc;
+  const int n_rep = mi_tensor_param_i32(dst, 0);
+  if (n_rep <= 0) return fail(MI_HIP_E_INVALID, "n_rep must be positive");
+  if (dst->ne[0] != v->ne[0] || dst->ne[1] != pr->ne[2] || dst->ne[2] != pr->ne[1])
+    return fail(MI_HIP_E_INVALID, "ATTN_KQV shapes are inconsistent");
+  if ((pr->ne[2] - 1) / n_rep >= v->ne[1] || pr->ne[0] > v->ne[2])
+    return fail(MI_HIP_E_INVALID, "ATTN_KQV reads outside the V tensor");
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_attn_kqv_node(view_of(dst), view_of(pr), view_of(v),
+                                          v->type == MI_TYPE_F16, n_rep,
+                                          static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "attn_kqv launch");
+}
+
+int mi_hip_op_attn_fused(mi_tensor* dst, void* stream) {
+  mi_hip_attn_args a;
+  int rc = fused_args_from_nodes(dst, &a);
+  if (rc) return rc;
+  a.stream = stream;
+  return mi_hip_attn_fwd(&a);
+}
+
+int mi_hip_graph_prepare(const mi_cgraph* graph) {
+  if (!graph || (graph->n_nodes > 0 && !graph->nodes))
+    return fail(MI_HIP_E_INVALID, "graph is NULL or has no node array");
+  std::lock_guard<std::mutex> lk(g_plan_mu);
+  g_readers.clear();
+  g_roles.clear();
+  for (int i = 0; i < graph->n_nodes; ++i) {
+    const mi_tensor* n = graph->nodes[i];
+    for (int s = 0; s < MI_MAX_SRC; ++s) {
+      const mi_tensor* src = n->src[s];
+      if (src && (src->op == MI_OP_ATTN_QK || src->op == MI_OP_SOFTMAX)) {
+        int32_t* c = g_readers.find(src, true);
+        if (!c) return fail(MI_HIP_E_UNSUPPORTED, "graph too large for the planner");
+        ++*c;
+      }
+    }
+  }
+  for (int i = 0; i < graph->n_nodes; ++i) {
+    const mi_tensor* kqv = graph->nodes[i];
+    if (kqv->op != MI_OP_ATTN_KQV) continue;
+    const mi_tensor* sm = kqv->src[0];
+    if (!sm || sm->op != MI_OP_SOFTMAX) continue;
+    const mi_tensor* qk = sm->src[0];
+    if (!qk || qk->op != MI_OP_ATTN_QK) continue;
+    int32_t* rs = g_readers.find(sm, false);
+    int32_t* rq = g_readers.find(qk, false);
+    if (!rs || !rq || *rs != 1 || *rq != 1) continue;
+    const Binding* bk = find_binding(qk->src[1]);
+    const Binding* bv = find_binding(kqv->src[1]);
+    if (!bk || !bv || bk->kv != bv->kv || bk->layer != bv->layer || bk->which != 0 || bv->which != 1)
+      continue;
+    int32_t* a = g_roles.find(qk, true);
+    int32_t* b = g_roles.find(sm, true);
+    int32_t* c = g_roles.find(kqv, true);
+    if (!a || !b || !c) return fail(MI_HIP_E_UNSUPPORTED, "graph too large for the planner");
+    *a = kFusedQK;
+    *b = kFusedSoftmax;
+    *c = kFusedKQV;
+  }
+  return MI_HIP_OK;
+}
+
+int mi_hip_compute_forward(mi_tensor* dst, int ith, int nth) {
+  (void)nth;
+  if (!dst) return 0;
+  switch (dst->op) {
+    case MI_OP_CPY: {
+      const mi_tensor* owner = dst->view_src ? dst->view_src : dst;
+      const Binding* b = find_binding(owner);
+      if (!b) return 0;
+      if (ith != 0) return 1;
+      mi_hip_kv* kv = b->kv;
+      const mi_tensor* src = dst->src[0];
+      if (!src || src->type != MI_TYPE_F32 || !src->data) {
+        fail(MI_HIP_E_INVALID, "CPY into the KV cache needs an F32 host source");
+        return -1;
+      }
+      if (dst->nb[2] != owner->nb[2] || dst->view_offs % owner->nb[2] != 0) {
+        fail(MI_HIP_E_INVALID, "CPY destination is not a whole-position view of the cache");
+        return -1;
+      }
+      if (src->ne[0] != kv->d.head_dim || src->ne[1] != kv->d.n_head_kv || src->ne[2] != dst->ne[2]) {
+        fail(MI_HIP_E_INVALID, "CPY source shape does not match the cache rows");
+        return -1;
+      }
+      const int pos0 = (int)(dst->view_offs / owner->nb[2]);
+      return mi_hip_kv_write(kv, b->layer, b->which, pos0, (int)dst->ne[2],
+                             static_cast<const float*>(src->data), src->nb, 0, kv->stream) == MI_HIP_OK
+                 ? 1
+                 : -1;
+    }
+    case MI_OP_ATTN_QK:
+    case MI_OP_SOFTMAX:
+    case MI_OP_ATTN_KQV: {
+      const int32_t role = role_of(dst);
+      if (role == kFusedQK || role == kFusedSoftmax) return 1;
+      if (role != kFusedKQV) {
+        const mi_tensor* kvsrc = dst->op == MI_OP_SOFTMAX ? nullptr : dst->src[1];
+        if (kvsrc && find_binding(kvsrc)) {
+          fail(MI_HIP_E_STATE,
+               "attention node reads a device-resident KV cache but is not part of a planned fused "
+               "chain (call mi_hip_graph_prepare after allocation)");
+          return -1;
+        }
+        return 0;
+      }
+      if (ith != 0) return 1;
+      const mi_tensor* sm = dst->src[0];
+      const mi_tensor* qk = sm->src[0];
+      const mi_tensor* q = qk->src[0];
+      const Binding* b = find_binding(qk->src[1]);
+      if (!b) {
+        fail(MI_HIP_E_STATE, "K tensor lost its binding");
+        return -1;
+      }
+      mi_hip_kv* kv = b->kv;
+      if (q->type != MI_TYPE_F32 || !contiguous3(q) || dst->type != MI_TYPE_F32 || !contiguous3(dst)) {
+        fail(MI_HIP_E_UNSUPPORTED, "host Q and output must be contiguous F32");
+        return -1;
+      }
+      const size_t n = (size_t)q->ne[0] * q->ne[1] * q->ne[2];
+      if (n > kv->q_floats || q->ne[0] != kv->d.head_dim) {
+        fail(MI_HIP_E_INVALID, "Q does not fit the cache's staging (n_ctx x n_head x head_dim)");
+        return -1;
+      }
+      if (bind_device()) return -1;
+      float* sq = kv->stage;
+      float* so = kv->stage + kv->q_floats;
+      mi_hip_attn_args a;
+      std::memset(&a, 0, sizeof a);
+      a.kv = kv;
+      a.layer = b->layer;
+      a.q = sq;
+      a.out = so;
+      a.q_nb[0] = a.out_nb[0] = 4;
+      a.q_nb[1] = a.out_nb[1] = 4 * (size_t)q->ne[0];
+      a.q_nb[2] = a.out_nb[2] = 4 * (size_t)q->ne[0] * q->ne[1];
+      a.n_head = (int32_t)q->ne[1];
+      a.n_rep = mi_tensor_param_i32(qk, 1);
+      a.n_past = mi_tensor_param_i32(qk, 0);
+      a.n_tokens = (int32_t)q->ne[2];
+      a.scale = mi_tensor_param_f32(sm, 1);
+      a.stream = kv->stream;
+      if (qk->ne[0] != (int64_t)a.n_past + a.n_tokens || mi_tensor_param_i32(sm, 0) != a.n_past) {
+        fail(MI_HIP_E_INVALID, "fused chain op_params disagree with the shapes");
+        return -1;
+      }
+      hipError_t e = hipMemcpyAsync(sq, q->data, n * sizeof(float), hipMemcpyHostToDevice, kv->stream);
+      if (e != hipSuccess) {
+        hip_fail(e, "hipMemcpyAsync(Q)");
+        return -1;
+      }
+      if (mi_hip_attn_fwd(&a) != MI_HIP_OK) return -1;
+      e = hipMemcpyAsync(dst->data, so, n * sizeof(float), hipMemcpyDeviceToHost, kv->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(kv->stream);
+      if (e != hipSuccess) {
+        hip_fail(e, "attention output copy");
+        return -1;
+      }
+      return 1;
+    }
+    default:
+      return 0;
+  }
+}
+
+}  // extern "C"

@@ -10,6 +10,7 @@
 // tests/golden/ and, where present, as the timed CPU baseline.
 #include <algorithm>
 #include <chrono>
+#include <cstddef>
 #include <cstdint>
 #include <vector>
 
@@ -102,6 +103,28 @@ int ref_softmax(const float* src, float* dst, int n_kv, int n_tokens, int n_head
 }
 
 float ref_fp16_to_fp32(uint16_t h) { return mi_fp16_to_fp32(h); }
+
+// The reference's own struct layout (src/tensor.h:122-160, src/graph.h:19-47),
+// in the order of mi_hip_abi_layout.
+int ref_abi_layout(size_t* out, int n) {
+  if (n < 15) return -1;
+  out[0] = sizeof(mi_tensor);
+  out[1] = offsetof(mi_tensor, type);
+  out[2] = offsetof(mi_tensor, ne);
+  out[3] = offsetof(mi_tensor, nb);
+  out[4] = offsetof(mi_tensor, op);
+  out[5] = offsetof(mi_tensor, op_params);
+  out[6] = offsetof(mi_tensor, src);
+  out[7] = offsetof(mi_tensor, data);
+  out[8] = offsetof(mi_tensor, view_src);
+  out[9] = offsetof(mi_tensor, view_offs);
+  out[10] = offsetof(mi_tensor, n_children);
+  out[11] = offsetof(mi_tensor, flags);
+  out[12] = offsetof(mi_tensor, name);
+  out[13] = offsetof(mi_tensor, extra);
+  out[14] = sizeof(mi_cgraph);
+  return 0;
+}
 
 void ref_fp16_to_fp32_row(const uint16_t* src, float* dst, int64_t n) {
   for (int64_t i = 0; i < n; ++i) dst[i] = mi_fp16_to_fp32(src[i]);

@@ -1,0 +1,222 @@
+"""GPU parity of the fused decode and prefill kernels against the oracle.
+
+Bar (written here, from the task's stated tolerance): |gpu - ref| <=
+1e-4 + 1e-4*|ref| for F32 K/V; 1e-2 for F16 K/V against unrounded inputs.
+With an F16 cache the oracle runs the engine's F32 ops on the exactly widened
+cache, and then the F32 bar applies too.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from conftest import TOL_F16, TOL_F32, case_inputs, load_golden
+from oracle import cpu_attention
+import mi_hip_attn as mh
+
+pytestmark = pytest.mark.gpu
+
+
+def assert_close(got, want, tol, what=""):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bound = tol["atol"] + tol["rtol"] * np.abs(want.astype(np.float64))
+    worst = float((err / bound).max()) if err.size else 0.0
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert worst <= 1.0, f"{what}: max abs err {err.max():.3e}, worst err/bound {worst:.3f}"
+
+
+def dev(a, dtype=None):
+    import torch
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if dtype is not None:
+        t = t.to(dtype)
+    return t.cuda()
+
+
+def fused(hip, stream, q, k, v, n_past, scale, f16=False):
+    """Runs mi_hip_attn_fwd on explicit device tensors; returns host output."""
+    import torch
+    assert k.shape == v.shape and k.shape[2] == q.shape[2] and q.shape[1] % k.shape[1] == 0
+    assert n_past + q.shape[0] <= k.shape[0]
+    dq = dev(q)
+    dk = dev(k.astype(np.float16)) if f16 else dev(k)
+    dv = dev(v.astype(np.float16)) if f16 else dev(v)
+    out = torch.full(q.shape, float("nan"), dtype=torch.float32, device="cuda")
+    a = mh.attn_args(dq, out, q.shape[1] // k.shape[1], n_past, scale, stream, k=dk, v=dv)
+    hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def ref_out(oracle, q, k, v, n_past, scale, f16=False, threads=16):
+    if f16:
+        k = cpu_attention.fp16_widen(k.astype(np.float16))
+        v = cpu_attention.fp16_widen(v.astype(np.float16))
+    return oracle.attention(q, k, v, n_past, scale, threads)[2]
+
+
+def test_golden_cases(hip, stream, golden_manifest):
+    for name, c in golden_manifest["cases"].items():
+        if c["head_dim"] not in (64, 128):
+            continue  # head_dim 4 (tiny model) runs through the node operators
+        print("case", name, flush=True)
+        q, k, v = case_inputs(c)
+        f16 = c["kv_type"] == "f16"
+        got = fused(hip, stream, q, k, v, c["n_past"], c["scale"], f16)
+        assert_close(got, load_golden(name)["out"], TOL_F32, name)
+        if f16:
+            unrounded = cpu_attention.oracle().attention(q, k, v, c["n_past"], c["scale"], 4)[2]
+            assert_close(got, unrounded, TOL_F16, name + " vs F32 inputs")
+
+
+@pytest.mark.parametrize("n_kv", [1, 63, 64, 65, 128, 1000, 1024, 4096, 16384, 32768])
+def test_decode_sweep_qwen05_shape(hip, stream, oracle, n_kv):
+    print("decode n_kv", n_kv, flush=True)
+    q, k, v = cpu_attention.make_inputs(1236 + n_kv, 64, 14, 2, n_kv, 1)
+    got = fused(hip, stream, q, k, v, n_kv - 1, 0.125)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, 0.125), TOL_F32, f"n_kv={n_kv}")
+
+
+@pytest.mark.parametrize("n_rep,hkv,d", [(1, 4, 64), (2, 2, 64), (4, 2, 128), (8, 2, 64),
+                                         (3, 2, 64), (6, 1, 128), (14, 1, 64)])
+def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d):
+    n_kv = 777
+    q, k, v = cpu_attention.make_inputs(31 + n_rep, d, n_rep * hkv, hkv, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F32)
+
+
+def test_decode_qwen7b_shape_f16_cache(hip, stream, oracle):
+    n_kv = 8192
+    q, k, v = cpu_attention.make_inputs(1238, 128, 28, 4, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(128)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=True), TOL_F32, "widened")
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
+
+
+def test_decode_batch_24_layers(hip, stream, oracle):
+    import torch
+    n_layers, n_kv = 24, 4096
+    qs, ks, vs, outs, items = [], [], [], [], []
+    for layer in range(n_layers):
+        q, k, v = cpu_attention.make_inputs(5000 + layer, 64, 14, 2, n_kv, 1)
+        qs.append(q)
+        ks.append(k)
+        vs.append(v)
+    dq = [dev(q) for q in qs]
+    dk = [dev(k) for k in ks]
+    dv = [dev(v) for v in vs]
+    douts = [torch.full((1, 14, 64), float("nan"), device="cuda") for _ in range(n_layers)]
+    for layer in range(n_layers):
+        items.append(mh.attn_args(dq[layer], douts[layer], 7, n_kv - 1 - layer, 0.125, stream,
+                                  k=dk[layer], v=dv[layer]))
+    arr = (mh.AttnArgs * n_layers)(*items)
+    hip.check(hip.mi_hip_attn_decode_batch(arr, n_layers, stream))
+    torch.cuda.synchronize()
+    for layer in range(n_layers):
+        want = ref_out(oracle, qs[layer], ks[layer], vs[layer], n_kv - 1 - layer, 0.125)
+        assert_close(douts[layer].cpu().numpy(), want, TOL_F32, f"layer {layer}")
+
+
+@pytest.mark.parametrize("n_past,n_tok,d,h,hkv", [
+    (0, 1024, 64, 14, 2),     # the prefill-1024 config, full oracle
+    (0, 33, 64, 14, 2),
+    (37, 100, 64, 14, 2),     # chunked prefill, n_past not a multiple of 32
+    (64, 96, 64, 4, 2),
+    (5, 200, 128, 8, 2),
+    (0, 500, 128, 28, 4),
+    (300, 2, 64, 14, 2),
+])
+def test_prefill_vs_oracle(hip, stream, oracle, n_past, n_tok, d, h, hkv):
+    print("prefill", n_past, n_tok, d, h, hkv, flush=True)
+    q, k, v = cpu_attention.make_inputs(777 + n_tok, d, h, hkv, n_past + n_tok + 3, n_tok)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_past, scale)
+    assert_close(got, ref_out(oracle, q, k, v, n_past, scale), TOL_F32)
+
+
+def test_prefill_f16_cache(hip, stream, oracle):
+    q, k, v = cpu_attention.make_inputs(4242, 64, 14, 2, 300, 257)
+    got = fused(hip, stream, q, k, v, 43, 0.125, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, 43, 0.125, f16=True), TOL_F32)
+
+
+def test_prefill_4096_rows_equal_decode_oracle(hip, stream, oracle):
+    # Size-independent property at the full n=4096: causal row j of a prefill
+    # is exactly a decode at n_past = j, which the oracle runs in O(n).
+    n = 4096
+    q, k, v = cpu_attention.make_inputs(1237 + 4096, 64, 14, 2, n, n)
+    got = fused(hip, stream, q, k, v, 0, 0.125)
+    for j in (0, 1, 31, 32, 33, 511, 1000, 2047, 3000, 4064, 4095):
+        want = oracle.attention(q[j:j + 1], k, v, j, 0.125, 8)[2]
+        assert_close(got[j:j + 1], want, TOL_F32, f"row {j}")
+
+
+def test_kv_cache_write_and_attend(hip, stream, oracle, golden_manifest):
+    import torch
+    for name in ("c1_decode", "prefill_chunked", "c4_f16_decode", "d128_prefill"):
+        c = golden_manifest["cases"][name]
+        q, k, v = case_inputs(c)
+        f16 = c["kv_type"] == "f16"
+        kv = hip.kv_create(2, c["n_ctx"], c["n_head_kv"], c["head_dim"], c["n_head"],
+                           mh.MI_TYPE_F16 if f16 else mh.MI_TYPE_F32)
+        try:
+            n_kv = c["n_past"] + c["n_tokens"]
+            nb = (ctypes.c_size_t * 3)(4, 4 * c["head_dim"], 4 * c["head_dim"] * c["n_head_kv"])
+            # K from the host in two pieces, V from the device in one.
+            kk = np.ascontiguousarray(k[:n_kv])
+            half = n_kv // 2
+            hip.check(hip.mi_hip_kv_write(kv, 1, 0, 0, half, kk.ctypes.data, nb, 0, None))
+            hip.check(hip.mi_hip_kv_write(kv, 1, 0, half, n_kv - half, kk[half:].ctypes.data,
+                                          nb, 0, None))
+            dvv = dev(v[:n_kv])
+            hip.check(hip.mi_hip_kv_write(kv, 1, 1, 0, n_kv, dvv.data_ptr(), nb, 1, stream))
+            dq = dev(q)
+            out = torch.full(q.shape, float("nan"), device="cuda")
+            a = mh.attn_args(dq, out, c["n_head"] // c["n_head_kv"], c["n_past"], c["scale"],
+                             stream, kv=kv, layer=1)
+            hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+            torch.cuda.synchronize()
+            assert_close(out.cpu().numpy(), load_golden(name)["out"], TOL_F32, name)
+            # The cache holds exactly the rounded rows in the engine layout.
+            ptr, ne, nbv = hip.kv_view(kv, 1, 0)
+            assert ne[:3] == [c["head_dim"], c["n_head_kv"], c["n_ctx"]]
+            assert nbv[0] == (2 if f16 else 4)
+            # Out-of-range requests fail cleanly.
+            a.n_past = c["n_ctx"]
+            assert hip.mi_hip_attn_fwd(ctypes.byref(a)) == 1
+            a.n_past, a.layer = c["n_past"], 2
+            assert hip.mi_hip_attn_fwd(ctypes.byref(a)) == 1
+            assert hip.mi_hip_kv_write(kv, 0, 0, c["n_ctx"], 1, kk.ctypes.data, nb, 0, None) == 1
+        finally:
+            hip.check(hip.mi_hip_kv_destroy(kv))
+
+
+def test_prefill_then_decode_equals_one_prefill(hip, stream):
+    # The engine's batch-vs-incremental check (tests/test_model_qwen2.cpp:87-134)
+    # restated for the attention path: one prefill of T tokens equals a
+    # prefill of the first P followed by T - P single-token decodes.
+    import torch
+    T, P = 70, 50
+    q, k, v = cpu_attention.make_inputs(8080, 64, 14, 2, 128, T)
+    kv = hip.kv_create(1, 128, 2, 64, 14)
+    try:
+        nb = (ctypes.c_size_t * 3)(4, 256, 512)
+        hip.check(hip.mi_hip_kv_write(kv, 0, 0, 0, T, np.ascontiguousarray(k[:T]).ctypes.data, nb, 0, None))
+        hip.check(hip.mi_hip_kv_write(kv, 0, 1, 0, T, np.ascontiguousarray(v[:T]).ctypes.data, nb, 0, None))
+        dq = dev(q)
+        whole = torch.zeros((T, 14, 64), device="cuda")
+        a = mh.attn_args(dq, whole, 7, 0, 0.125, stream, kv=kv, layer=0)
+        hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+        parts = torch.zeros((T, 14, 64), device="cuda")
+        a = mh.attn_args(dq[:P], parts[:P], 7, 0, 0.125, stream, kv=kv, layer=0)
+        hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+        for j in range(P, T):
+            a = mh.attn_args(dq[j:j + 1], parts[j:j + 1], 7, j, 0.125, stream, kv=kv, layer=0)
+            hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+        torch.cuda.synchronize()
+        assert_close(parts.cpu().numpy(), whole.cpu().numpy(), dict(atol=2e-6, rtol=2e-6))
+    finally:
+        hip.check(hip.mi_hip_kv_destroy(kv))

@@ -1,0 +1,187 @@
+"""Pins the CPU oracle (oracle/attn_oracle.cpp) before anything is compared to it.
+
+1. Golden vectors: outputs of the reference's own ops (compiled in place from
+   src/ops_cpu.cpp etc., see tests/golden/make_golden.py) -- bit-exact, at
+   several thread counts (the static split of src/ops_cpu.cpp:46-53 never
+   changes a result).
+2. Mathematics the reference's output is fixed by, chosen so that a plausible
+   slip (wrong GQA index, transposed operand, off-by-one mask, missing scale)
+   fails: float64 brute force, one-hot known answers, invariants.
+3. The reference's own known-answer softmax test (tests/test_ops_cpu.cpp:215-241).
+"""
+import numpy as np
+import pytest
+
+from conftest import case_inputs, load_golden
+from oracle import cpu_attention
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def f16_cache(k, v):
+    return (cpu_attention.fp16_widen(k.astype(np.float16)),
+            cpu_attention.fp16_widen(v.astype(np.float16)))
+
+
+@pytest.mark.parametrize("n_threads", [1, 3, 8])
+def test_oracle_matches_reference_goldens_bitwise(oracle, golden_manifest, n_threads):
+    for name, c in golden_manifest["cases"].items():
+        q, k, v = case_inputs(c)
+        if c["kv_type"] == "f16":
+            k, v = f16_cache(k, v)
+        scores, probs, out = oracle.attention(q, k, v, c["n_past"], c["scale"], n_threads)
+        g = load_golden(name)
+        assert np.array_equal(bits(out), bits(g["out"])), name
+        if "scores" in g:
+            assert np.array_equal(bits(scores), bits(g["scores"])), name
+            assert np.array_equal(bits(probs), bits(g["probs"])), name
+
+
+def test_golden_files_are_what_the_manifest_recorded(golden_manifest):
+    for name, c in golden_manifest["cases"].items():
+        g = load_golden(name)
+        for key, digest in c["sha256"].items():
+            assert cpu_attention.sha256(g[key]) == digest, (name, key)
+
+
+def test_softmax_known_answer_from_reference_tests(oracle):
+    # tests/test_ops_cpu.cpp:215-241: [n_kv=4, n_tokens=2], masked 99s never leak.
+    import ctypes
+    from mi_hip_attn import make_tensor, MI_OP_SOFTMAX
+    src = np.array([5, 99, 99, 99, 1, 3, 99, 99], np.float32)
+    dst = np.full(8, np.nan, np.float32)
+    s = make_tensor(src.ctypes.data, [4, 2, 1], [4, 16, 32])
+    d = make_tensor(dst.ctypes.data, [4, 2, 1], [4, 16, 32], op=MI_OP_SOFTMAX, src=[s],
+                    params=[0, 1.0])
+    fn = oracle.lib.oracle_softmax
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
+    fn(ctypes.addressof(d), 0, 1)
+    assert dst[0] == 1.0 and dst[1] == 0 and dst[2] == 0 and dst[3] == 0
+    e0, e1 = np.exp(np.float32(-2.0)), np.float32(1.0)
+    assert abs(dst[4] - e0 / (e0 + e1)) < 1e-6 and abs(dst[5] - e1 / (e0 + e1)) < 1e-6
+    assert dst[6] == 0 and dst[7] == 0
+    g = load_golden("softmax_kat")
+    assert np.array_equal(bits(dst), bits(g["probs"].reshape(-1)))
+
+
+def test_fp16_widening_is_exact_for_every_code(golden_manifest):
+    codes = np.arange(65536, dtype=np.uint16)
+    ours = cpu_attention.fp16_widen(codes)
+    numpy_ref = codes.view(np.float16).astype(np.float32)  # IEEE widening, a library routine
+    assert np.array_equal(bits(ours), bits(numpy_ref))
+    # ... and the reference's own converter (src/quant.cpp:26-63) over all codes.
+    assert cpu_attention.sha256(bits(ours)) == golden_manifest["fp16_lut_sha256"]
+
+
+@pytest.mark.parametrize("n,nth", [(0, 1), (1, 4), (7, 3), (100, 8), (14 * 512, 16), (5, 8)])
+def test_split_range_partitions_with_remainder_first(oracle, n, nth):
+    spans = [oracle.split_range(n, i, nth) for i in range(nth)]
+    assert spans[0][0] == 0 and spans[-1][1] == n
+    for (a, b), (c, _) in zip(spans, spans[1:]):
+        assert b == c
+    sizes = [b - a for a, b in spans]
+    assert max(sizes) - min(sizes) <= 1
+    assert sizes == sorted(sizes, reverse=True)  # the extra units go to the front
+
+
+def brute_force(q, k, v, n_past, scale):
+    """float64 attention straight from the definitions (causal, GQA h -> h // n_rep)."""
+    t, h, d = q.shape
+    n_kv = n_past + t
+    n_rep = h // k.shape[1]
+    q64, k64, v64 = (x.astype(np.float64) for x in (q, k, v))
+    scores = np.zeros((h, t, n_kv))
+    probs = np.zeros((h, t, n_kv))
+    out = np.zeros((t, h, d))
+    for hh in range(h):
+        g = hh // n_rep
+        for j in range(t):
+            s = k64[:n_kv, g, :] @ q64[j, hh, :]
+            scores[hh, j] = s
+            vis = n_past + j + 1
+            x = s[:vis] * scale
+            e = np.exp(x - x.max())
+            probs[hh, j, :vis] = e / e.sum()
+            out[j, hh] = probs[hh, j] @ v64[:n_kv, g, :]
+    return scores, probs, out
+
+
+@pytest.mark.parametrize("shape", [
+    # head_dim, n_head, n_head_kv, n_ctx, n_past, n_tokens
+    (4, 2, 1, 9, 0, 5),
+    (64, 14, 2, 40, 3, 6),
+    (64, 14, 2, 80, 79, 1),
+    (128, 8, 2, 30, 0, 17),
+    (32, 6, 3, 12, 4, 4),
+])
+def test_oracle_matches_float64_definition(oracle, shape):
+    d, h, hkv, n_ctx, n_past, t = shape
+    q, k, v = cpu_attention.make_inputs(99 + d + h, d, h, hkv, n_ctx, t)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    s, p, o = oracle.attention(q, k, v, n_past, scale, 2)
+    s64, p64, o64 = brute_force(q, k, v, n_past, scale)
+    assert np.allclose(s, s64, rtol=1e-5, atol=1e-5)
+    assert np.allclose(p, p64, rtol=1e-5, atol=1e-6)
+    assert np.allclose(o, o64, rtol=1e-5, atol=1e-5)
+
+
+def test_brute_force_check_catches_planted_mistakes(oracle):
+    # The comparison above must fail for the classic slips: a wrong GQA index
+    # (h % n_hkv instead of h // n_rep) and an off-by-one causal boundary.
+    d, h, hkv, n_ctx, n_past, t = 16, 4, 2, 12, 2, 5
+    q, k, v = cpu_attention.make_inputs(7, d, h, hkv, n_ctx, t)
+    scale = 0.25
+    s, p, o = oracle.attention(q, k, v, n_past, scale, 1)
+    s64, p64, o64 = brute_force(q, k, v, n_past, scale)
+    wrong_gqa = s.copy()
+    for hh in range(h):
+        wrong_gqa[hh] = (k[: n_past + t, hh % hkv, :] @ q[:, hh, :].T).T
+    assert not np.allclose(wrong_gqa, s64, rtol=1e-5, atol=1e-5)
+    shifted = np.roll(p, 1, axis=2)  # mask one key too late
+    assert not np.allclose(shifted, p64, rtol=1e-5, atol=1e-6)
+
+
+def test_invariants(oracle):
+    d, h, hkv, n_ctx = 64, 14, 2, 48
+    n_rep = h // hkv
+    q, k, v = cpu_attention.make_inputs(5, d, h, hkv, n_ctx, 8)
+    scale = 0.125
+    # One-hot query e_3 returns K's column 3 exactly (scores are plain sums).
+    q1 = np.zeros_like(q)
+    q1[:, :, 3] = 1.0
+    s, p, o = oracle.attention(q1, k, v, 40, scale, 1)
+    for hh in range(h):
+        assert np.array_equal(s[hh, 0], k[:48, hh // n_rep, 3])
+    # Identical queries in one GQA group give identical scores.
+    q2 = q.copy()
+    q2[:, 1:n_rep, :] = q2[:, :1, :]
+    s, p, o = oracle.attention(q2, k, v, 40, scale, 1)
+    for hh in range(1, n_rep):
+        assert np.array_equal(s[hh], s[0])
+    # Rows sum to one, masked tail exactly zero, decode never masks.
+    s, p, o = oracle.attention(q, k, v, 40, scale, 1)
+    assert np.allclose(p.sum(axis=2), 1.0, atol=1e-6)
+    for j in range(8):
+        assert np.all(p[:, j, 40 + j + 1:] == 0.0)
+    s, p, o = oracle.attention(q[:1], k, v, 47, scale, 1)
+    assert np.all(p > 0)
+    # A single visible key gives probability exactly 1 and the V row exactly.
+    s, p, o = oracle.attention(q[:1], k, v, 0, scale, 1)
+    assert np.all(p == 1.0)
+    for hh in range(h):
+        assert np.array_equal(o[0, hh], v[0, hh // n_rep])
+    # Permuting cached positions permutes the scores (decode).
+    perm = np.random.default_rng(1).permutation(48)
+    s0, _, o0 = oracle.attention(q[:1], k, v, 47, scale, 1)
+    s1, _, o1 = oracle.attention(q[:1], k[perm], v[perm], 47, scale, 1)
+    assert np.array_equal(s1, s0[:, :, perm])
+    assert np.allclose(o1, o0, atol=1e-6)
+    # Scale enters only through the softmax: scores ignore it, probabilities
+    # at scale s equal the probabilities of the scores pre-multiplied by s.
+    s_a, p_a, _ = oracle.attention(q[:1], k, v, 47, 0.5, 1)
+    s_b, p_b, _ = oracle.attention(q[:1] * np.float32(0.5), k, v, 47, 1.0, 1)
+    s_c, _, _ = oracle.attention(q[:1], k, v, 47, 2.0, 1)
+    assert np.array_equal(s_a, s_c)
+    assert np.allclose(p_a, p_b, rtol=1e-5, atol=1e-7)
