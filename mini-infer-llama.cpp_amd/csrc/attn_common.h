@@ -39,9 +39,9 @@ struct DecodeParams {
   int32_t n_head_kv;
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
   int32_t splits;       // position splits per (item, head chunk)
+  int32_t waves;        // waves per workgroup (1..kDecodeWaves)
   float scale_log2e;    // softmax scale * log2(e)
-  float* part;          // split partials (splits > 1)
-  unsigned* counter;    // arrival counters, one per (item, head chunk); self-resetting
+  float* part;          // split records (splits > 1), merged by decode_merge_kernel
 };
 
 // ---------------------------------------------------------------------------
@@ -60,20 +60,9 @@ struct PrefillParams {
   int64_t q_s1, q_s2;              // bytes between heads, between tokens
   int64_t o_s1, o_s2;
   int32_t n_head, n_rep, n_past, n_tokens;
-  int32_t chunk_tiles;   // key tiles per unit (C)
   int32_t n_qblocks;     // ceil(n_tokens / 32)
-  int32_t units_per_head;
-  int32_t n_units;       // n_head * units_per_head
   float scale_log2e;
-  float* part;           // per-unit partials
-  unsigned* counter;     // per (head, q-block); self-resetting
 };
-
-// Prefix sum sum_{t=1..x} ceil(t / c) in closed form.
-__host__ __device__ inline int64_t ceil_prefix(int64_t x, int64_t c) {
-  const int64_t a = x / c, b = x % c;
-  return c * a * (a + 1) / 2 + b * (a + 1);
-}
 
 // ---------------------------------------------------------------------------
 // Device helpers.
@@ -91,6 +80,49 @@ __device__ inline float wave_sum(float x) {
 }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// DPP lane moves (VALU, no LDS). Within each row of 16 lanes:
+//   xor1 / xor2: quad_perm [1,0,3,2] / [2,3,0,1]; half_mirror: i <-> 7-i;
+//   mirror: i <-> 15-i; bcast<J>: lane J of the row to the whole row.
+template <int CTRL>
+__device__ inline float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+template <int J>
+__device__ inline float row_bcast(float x) { return dpp_mov<0x150 + J>(x); }
+
+// acc + bcast_J(q) * k in ONE instruction: v_fmac_f32 with a DPP row_newbcast
+// source operand (lane J of each row of 16 supplies q to the whole row). The
+// compiler does not form this itself (the accumulator is tied), hence asm.
+// Callers never write q with a VALU instruction right before (q comes from a
+// load), so the DPP source-read wait states are met.
+template <int J>
+__device__ inline float fmac_bcast(float acc, float q, float k) {
+  asm("v_fmac_f32_dpp %0, %1, %2 row_newbcast:%3 row_mask:0xf bank_mask:0xf"
+      : "+v"(acc)
+      : "v"(q), "v"(k), "i"(J));
+  return acc;
+}
+
+// Max over the 16 lanes of each row, left in every lane of the row.
+__device__ inline float row_max16(float x) {
+  x = fmaxf(x, dpp_mov<0xB1>(x));   // quad_perm [1,0,3,2]
+  x = fmaxf(x, dpp_mov<0x4E>(x));   // quad_perm [2,3,0,1]
+  x = fmaxf(x, dpp_mov<0x141>(x));  // row_half_mirror
+  x = fmaxf(x, dpp_mov<0x140>(x));  // row_mirror
+  return x;
+}
+
+// Max over the wave, wave-uniform result: rows by DPP, then the four row
+// maxima through readlane (no LDS traffic).
+__device__ inline float wave_max_dpp(float x) {
+  x = row_max16(x);
+  const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0));
+  const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16));
+  const float c = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32));
+  const float d = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
 
 // Orders this wave's LDS accesses (the wave executes LDS operations in issue
 // order; this stops the compiler from moving them across the point).

@@ -8,71 +8,43 @@
 //   grid.x = split of the positions [0, n_kv) (split-KV); each workgroup's
 //            kDecodeWaves waves take interleaved 64-position tiles of its
 //            split and keep a running (max, sum, acc) per head.
-// Per 64-position tile, one wave:
-//   1. streams the tile's V rows into registers (coalesced 16-byte loads,
-//      D/4 lanes per row) so their latency overlaps the QK work;
-//   2. stages K rows 64 dims at a time through a padded LDS tile and then
-//      lets lane i own position i: each lane dots its row with the G query
-//      vectors, which are wave-uniform and read through the scalar cache;
-//   3. updates the running max with a wave reduction, rescales, exponentiates
-//      (exp2 of log2e-prescaled scores) and writes the probabilities to LDS;
+// The wave's G query vectors stay in registers for the whole kernel, spread
+// over the 16 lanes of each row. Per 64-position tile, one wave:
+//   1. requests the tile's K rows (coalesced 16-byte loads);
+//   2. stages K rows 64 dims at a time through a swizzled LDS tile and lets
+//      lane i own position i: each lane dots its row with the G queries, whose
+//      elements reach every lane as DPP row-broadcast FMA operands;
+//   3. requests the tile's V rows, updates the running max (DPP row
+//      reduction + readlane, no LDS),
+//      rescales, exponentiates (exp2 of log2e-prescaled scores) and writes
+//      the probabilities to LDS;
 //   4. accumulates P.V with lanes owning 4 output dims of one row.
-// Waves of a workgroup merge through LDS; splits merge through a workspace:
-// the last workgroup of an (item, head chunk) to arrive (device-scope
-// counter) combines all split partials with the stable rescaling
-// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s and resets the counter.
+// Waves of a workgroup merge through LDS. With one split the workgroup writes
+// the output; otherwise it writes an (m, l, acc) record per head to the
+// workspace and decode_merge_kernel, launched next on the same stream,
+// combines the splits with the stable rescaling
+// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s.
+// (No cross-workgroup signalling inside a kernel: on this part a device-scope
+// fence writes back and invalidates the whole L2 of the XCD.)
+#include <cstdlib>
+
 #include "attn_common.h"
 #include "kernels.h"
 
 namespace mi {
 
-// One 16-byte LDS slot per lane of the K tile (lane l of the instruction
-// whose wave-uniform base is `dst` lands at dst + 4*l floats).
-template <typename KT>
-__device__ inline void stage_k_slot(const char* src, float* dst, int lane);
-
-// F32 cache: direct global -> LDS transfer, no register staging.
-template <>
-__device__ inline void stage_k_slot<float>(const char* src, float* dst, int lane) {
-  (void)lane;
-  __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(src),
-                                   (__attribute__((address_space(3))) void*)(dst),
-                                   16, 0, 0);
-}
-
-// F16 cache: 8-byte load, exact widening, 16-byte LDS store.
-template <>
-__device__ inline void stage_k_slot<_Float16>(const char* src, float* dst, int lane) {
-  *reinterpret_cast<float4*>(dst + 4 * lane) = load4<_Float16>(src);
-}
-
-// (The compiler's wait-count pass tracks the direct-to-LDS transfers and
-// waits for them before the first LDS read of the tile.)
-
-// qa[h][0..3] = Q[head0 + h][4*step .. 4*step+3] through the scalar cache.
-template <int G>
-__device__ inline void load_q4(float (&qa)[G][4], const float* qrow, int64_t q_s1f, int step) {
-  const const_f32_ptr qc = as_const(qrow);
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) qa[h][e] = qc[h * q_s1f + step * 4 + e];
-}
-
 template <int D, typename KT, int G>
-__global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel(const DecodeParams p) {
+__device__ __forceinline__ void decode_body(const DecodeParams& p) {
   constexpr int ELT = (int)sizeof(KT);
   constexpr int NCH = D / 64;                    // 64-dim chunks staged for QK
   constexpr int LPR = D / 4;                     // PV: lanes per cache row
   constexpr int RPI = kWave / LPR;               // PV: rows per load instruction
   constexpr int NV = kDecodeTile / RPI;          // PV: load instructions per tile
-  constexpr int NV0 = NV < 16 ? NV : 16;         // of which issued before QK
   constexpr int TS = kDecodeTile * 64;  // LDS floats per wave (swizzled, unpadded)
   constexpr int HDR = (2 * G + 3) & ~3;          // record header: m[G], l[G]
   constexpr int REC = HDR + G * D;               // one merge record
 
   extern __shared__ float lds[];
-  __shared__ int s_last;
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -116,77 +88,99 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel(const Decod
   const int ks2 = (int)it.k_s2, vs2 = (int)it.v_s2;
   const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
+  // The G query vectors, spread over the 16 lanes of every row:
+  // qv[h][c] = Q[head0 + h][16 c + (lane & 15)]. A DPP row broadcast hands
+  // dim 16 c + j to every lane as an FMA operand: no memory round trip.
+  float qv[G][D / 16];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) qv[h][c] = q0[h * q_s1f + 16 * c + (lane & 15)];
+
   for (int p0 = lo + wave * kDecodeTile; p0 < hi; p0 += nwaves * kDecodeTile) {
     const int nvalid = min(kDecodeTile, hi - p0);
     const int last = nvalid - 1;
     const char* ktile = kbase + (int64_t)p0 * it.k_s2;  // wave-uniform
     const char* vtile = vbase + (int64_t)p0 * it.v_s2;
 
-    float4 vreg[NV];
     float s[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) s[h] = 0.f;
+    float4 vreg[NV];
 
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      // Stage rows p0..p0+63, dims [64c, 64c+64) of KV head g into the wave's
-      // LDS tile. Row r is 256 contiguous bytes; its 16-byte slot s holds the
-      // row's chunk s ^ (r & 15), so lane r reading chunk d4 of its own row
-      // (slot d4 ^ (r & 15)) hits 16 distinct bank groups across 16 lanes.
-      // Rows past the split end re-read its last row (their scores are masked).
+      // Rows p0..p0+63, dims [64c, 64c+64) of KV head g: row r is 256
+      // contiguous LDS bytes whose 16-byte slot s holds chunk s ^ (r & 15),
+      // so lane r reading chunk d of its own row hits 16 distinct bank groups
+      // across 16 lanes. Rows past the split end re-read its last row (their
+      // scores are masked).
+      float4 kreg[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const unsigned off = (unsigned)(min(i * 4 + kr, last) * ks2 + (c * 64 + kc * 4) * ELT);
+        kreg[i] = load4<KT>(ktile + off);
+      }
       wave_lds_fence();
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = i * 4 + kr;
-        const unsigned off =
-            (unsigned)(min(row, last) * ks2 + (c * 64 + ((kc ^ (row & 15)) * 4)) * ELT);
-        stage_k_slot<KT>(ktile + off, klds + i * 256, lane);
-      }
-      // Keep every K transfer ahead of the V loads in issue order, so that
-      // waiting for K leaves the V loads in flight.
-      asm volatile("" ::: "memory");
-      if (c == 0) {
-        // V rows of the tile: in flight during the QK work.
-#pragma unroll
-        for (int i = 0; i < NV0; ++i) {
-          const int row = i * RPI + vr;
-          const unsigned off = (unsigned)(min(row, last) * vs2 + vc * 4 * ELT);
-          const float4 x = load4<KT>(vtile + off);
-          vreg[i] = row < nvalid ? x : zero4;
-        }
+        *reinterpret_cast<float4*>(&klds[row * 64 + ((kc ^ (row & 15)) * 4)]) = kreg[i];
       }
       wave_lds_fence();
 
-      // Q for this chunk is wave-uniform: scalar loads, pipelined one
-      // 4-dim step ahead through a pointer the compiler may not hoist.
-      const float* qrow = q0 + c * 64;
-      float qa[G][4], qn[G][4];
-      load_q4<G>(qa, qrow, q_s1f, 0);
+      // Lane = position: dot its row with the G queries. (qv passes through an
+      // empty asm so the broadcasts stay here instead of being hoisted out of
+      // the tile loop, which would need one register per broadcast value.)
 #pragma unroll
-      for (int d4 = 0; d4 < 16; ++d4) {
-        if (d4 + 1 < 16) {
-          asm volatile("" : "+s"(qrow));
-          load_q4<G>(qn, qrow, q_s1f, d4 + 1);
-        }
-        const float4 kv = *reinterpret_cast<const float4*>(
-            &klds[lane * 64 + ((d4 ^ (lane & 15)) * 4)]);
+      for (int q16 = 0; q16 < 4; ++q16) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) asm volatile("" : "+v"(qv[h][c * 4 + q16]));
+        const float4 k0 = *reinterpret_cast<const float4*>(
+            &klds[lane * 64 + (((4 * q16 + 0) ^ (lane & 15)) * 4)]);
+        const float4 k1 = *reinterpret_cast<const float4*>(
+            &klds[lane * 64 + (((4 * q16 + 1) ^ (lane & 15)) * 4)]);
+        const float4 k2 = *reinterpret_cast<const float4*>(
+            &klds[lane * 64 + (((4 * q16 + 2) ^ (lane & 15)) * 4)]);
+        const float4 k3 = *reinterpret_cast<const float4*>(
+            &klds[lane * 64 + (((4 * q16 + 3) ^ (lane & 15)) * 4)]);
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          s[h] = fmaf(kv.x, qa[h][0], s[h]);
-          s[h] = fmaf(kv.y, qa[h][1], s[h]);
-          s[h] = fmaf(kv.z, qa[h][2], s[h]);
-          s[h] = fmaf(kv.w, qa[h][3], s[h]);
-        }
-        if (d4 + 1 < 16) {
-#pragma unroll
-          for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) qa[h][e] = qn[h][e];
+          const float qq = qv[h][c * 4 + q16];
+          float a = s[h];
+          a = fmac_bcast<0>(a, qq, k0.x);
+          a = fmac_bcast<1>(a, qq, k0.y);
+          a = fmac_bcast<2>(a, qq, k0.z);
+          a = fmac_bcast<3>(a, qq, k0.w);
+          a = fmac_bcast<4>(a, qq, k1.x);
+          a = fmac_bcast<5>(a, qq, k1.y);
+          a = fmac_bcast<6>(a, qq, k1.z);
+          a = fmac_bcast<7>(a, qq, k1.w);
+          a = fmac_bcast<8>(a, qq, k2.x);
+          a = fmac_bcast<9>(a, qq, k2.y);
+          a = fmac_bcast<10>(a, qq, k2.z);
+          a = fmac_bcast<11>(a, qq, k2.w);
+          a = fmac_bcast<12>(a, qq, k3.x);
+          a = fmac_bcast<13>(a, qq, k3.y);
+          a = fmac_bcast<14>(a, qq, k3.z);
+          a = fmac_bcast<15>(a, qq, k3.w);
+          s[h] = a;
         }
       }
     }
 
-    // Online softmax: wave-uniform running max per head, per-lane partial sums.
+    // V rows of the tile (requested after QK so that the V and K register
+    // sets never coexist; other waves cover the latency).
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int row = i * RPI + vr;
+      const unsigned off = (unsigned)(min(row, last) * vs2 + vc * 4 * ELT);
+      const float4 x = load4<KT>(vtile + off);
+      vreg[i] = row < nvalid ? x : zero4;
+    }
+
+    // Online softmax: wave-uniform running max per head (DPP + readlane),
+    // per-lane partial sums.
     const bool valid = lane < nvalid;
     float pv[8];
 #pragma unroll
@@ -194,7 +188,7 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel(const Decod
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       const float x = valid ? s[h] * p.scale_log2e : -INFINITY;
-      const float mn = fmaxf(m[h], wave_max(x));
+      const float mn = fmaxf(m[h], wave_max_dpp(x));
       const float alpha = fast_exp2(m[h] - mn);
       const float e = fast_exp2(x - mn);
       l[h] = l[h] * alpha + e;
@@ -210,14 +204,6 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel(const Decod
     if (G > 4)
       *reinterpret_cast<float4*>(&klds[lane * 8 + 4]) = make_float4(pv[4], pv[5], pv[6], pv[7]);
     wave_lds_fence();
-
-#pragma unroll
-    for (int i = NV0; i < NV; ++i) {
-      const int row = i * RPI + vr;
-      const unsigned off = (unsigned)(min(row, last) * vs2 + vc * 4 * ELT);
-      const float4 x = load4<KT>(vtile + off);
-      vreg[i] = row < nvalid ? x : zero4;
-    }
 
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -293,46 +279,104 @@ __global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel(const Decod
       }
     }
   }
-  if (direct) return;
+}
 
-  // Split merge by the last workgroup to arrive.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned prev = atomicAdd(&p.counter[grp], 1u);
-    s_last = prev == (unsigned)(p.splits - 1);
+// Two occupancy variants of the same body: two waves per SIMD (register
+// budget 256) or one (512).
+template <int D, typename KT, int G>
+__global__ __launch_bounds__(kDecodeWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_kernel(const DecodeParams p) {
+  decode_body<D, KT, G>(p);
+}
+
+template <int D, typename KT, int G>
+__global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel_wide(const DecodeParams p) {
+  decode_body<D, KT, G>(p);
+}
+
+// Combines the split records of one (item, head chunk) per workgroup in two
+// passes: per head the max m over splits, the weights w_s = 2^(m_s - m) and
+// the denominator; then every (head, dim) output is an independent weighted
+// sum over the splits' unnormalised accumulators.
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p) {
+  constexpr int HDR = (2 * G + 3) & ~3;
+  constexpr int REC = HDR + G * D;
+  extern __shared__ float lds[];  // w[G][splits], inv_l[G]
+  const int grp = blockIdx.x;
+  const int per_item = p.n_head_kv * p.n_chunks;
+  const DecodeItem& it = p.item[grp / per_item];
+  const int g = (grp % per_item) / p.n_chunks;
+  const int hc = grp % p.n_chunks;
+  const int head0 = g * p.n_rep + hc * G;
+  const int S = p.splits;
+  const float* base = p.part + (int64_t)grp * S * REC;
+  float* w = lds;
+  float* inv_l = lds + G * S;
+
+  // pass 1: one wave per head (round robin), lanes over splits
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  for (int h = wv; h < G; h += blockDim.x / kWave) {
+    float mx = -INFINITY;
+    for (int sp = lane; sp < S; sp += kWave) mx = fmaxf(mx, base[(int64_t)sp * REC + h]);
+    mx = wave_max_dpp(mx);
+    float den = 0.f;
+    for (int sp = lane; sp < S; sp += kWave) {
+      const float* r = base + (int64_t)sp * REC;
+      const float wt = fast_exp2(r[h] - mx);  // empty split: m = -inf -> 0
+      w[h * S + sp] = wt;
+      den += wt * r[G + h];
+    }
+    den = wave_sum(den);
+    if (lane == 0) inv_l[h] = 1.f / den;
   }
   __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float* gbase = p.part + (int64_t)grp * p.splits * REC;
+
+  // pass 2: independent weighted sums
   for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
     const int h = idx / D, d = idx % D;
-    float mx = -INFINITY;
-    for (int sp = 0; sp < p.splits; ++sp) mx = fmaxf(mx, gbase[sp * REC + h]);
-    float a = 0.f, sum = 0.f;
-    for (int sp = 0; sp < p.splits; ++sp) {
-      const float* r = gbase + sp * REC;
-      const float sc = fast_exp2(r[h] - mx);
-      a += sc * r[HDR + h * D + d];
-      sum += sc * r[G + h];
+    const float* a = base + HDR + h * D + d;
+    const float* wh = w + h * S;
+    // 8 independent loads per round keep the split records' latency overlapped.
+    float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int sp = 0;
+    for (; sp + 8 <= S; sp += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc8[u] = fmaf(wh[sp + u], a[(int64_t)(sp + u) * REC], acc8[u]);
     }
+    for (; sp < S; ++sp) acc8[0] = fmaf(wh[sp], a[(int64_t)sp * REC], acc8[0]);
     float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) +
                                         (int64_t)(head0 + h) * it.o_s1);
-    o[d] = a / sum;
+    o[d] = (((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]))) *
+           inv_l[h];
   }
-  if (threadIdx.x == 0) p.counter[grp] = 0u;
 }
 
 template <int D, typename KT, int G>
 static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
-  const size_t lds = (size_t)kDecodeWaves * kDecodeTile * 64 * sizeof(float);
+  const size_t lds_max = (size_t)kDecodeWaves * kDecodeTile * 64 * sizeof(float);
+  // head_dim 64: two waves per SIMD unless MI_HIP_DECODE_WIDE=1; head_dim 128: one.
+  static const bool wide = D > 64 || [] {
+    const char* e = std::getenv("MI_HIP_DECODE_WIDE");
+    return e && e[0] == '1';
+  }();
+  const void* fn = wide ? reinterpret_cast<const void*>(&decode_kernel_wide<D, KT, G>)
+                        : reinterpret_cast<const void*>(&decode_kernel<D, KT, G>);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&decode_kernel<D, KT, G>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
   if (attr != hipSuccess) return attr;
-  const dim3 grid((unsigned)p.splits, (unsigned)(p.n_items * p.n_head_kv * p.n_chunks));
-  hipLaunchKernelGGL((decode_kernel<D, KT, G>), grid, dim3(kDecodeWaves * kWave), lds, stream, p);
+  const unsigned groups = (unsigned)(p.n_items * p.n_head_kv * p.n_chunks);
+  const size_t lds = (size_t)p.waves * kDecodeTile * 64 * sizeof(float);
+  if (wide)
+    hipLaunchKernelGGL((decode_kernel_wide<D, KT, G>), dim3((unsigned)p.splits, groups),
+                       dim3(p.waves * kWave), lds, stream, p);
+  else
+    hipLaunchKernelGGL((decode_kernel<D, KT, G>), dim3((unsigned)p.splits, groups),
+                       dim3(p.waves * kWave), lds, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.splits == 1) return e;
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(groups), dim3(256),
+                     ((size_t)G * p.splits + G) * sizeof(float), stream, p);
   return hipGetLastError();
 }
 

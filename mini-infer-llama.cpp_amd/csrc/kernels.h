@@ -17,7 +17,6 @@ hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int grou
                          hipStream_t stream);
 
 // prefill.hip
-size_t prefill_record_floats(int head_dim);             // floats per unit partial
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, hipStream_t stream);
 
 // nodes.hip -- node-level kernels on device tensors (byte strides).

@@ -5,7 +5,8 @@
 // materialise scores and probabilities exactly like the CPU graph does, so a
 // caller can run any single ATTN_QK, SOFTMAX or ATTN_KQV node on the GPU.
 // ATTN_QK and ATTN_KQV accumulate with separately rounded multiply and add
-// (__fmul_rn/__fadd_rn: no fused multiply-add) in the reference's order --
+// (floating-point contraction is switched off in their bodies, so no fused
+// multiply-add is formed) in the reference's order --
 // d ascending for scores, t ascending over all keys for the output -- so on
 // identical inputs they reproduce src/ops_cpu.cpp:356-380 and :386-410 bit
 // for bit. SOFTMAX uses the device expf and a tree sum, so it matches
@@ -27,6 +28,7 @@ __device__ inline float& at(const NodeView& t, int64_t i0, int64_t i1, int64_t i
 // dst [n_kv, n_tokens, n_head]: S[i,j,h] = sum_d K[d, h/n_rep, i] * Q[d, h, j].
 template <typename KT>
 __global__ void attn_qk_node_kernel(NodeView dst, NodeView q, NodeView k, int n_rep) {
+#pragma clang fp contract(off)
   const int64_t n_kv = dst.ne[0], n_tok = dst.ne[1], n_head = dst.ne[2], dim = q.ne[0];
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= n_kv * n_tok * n_head) return;
@@ -35,36 +37,38 @@ __global__ void attn_qk_node_kernel(NodeView dst, NodeView q, NodeView k, int n_
   const int64_t h = idx / (n_kv * n_tok);
   const int64_t g = h / n_rep;
   float acc = 0.f;
-  for (int64_t d = 0; d < dim; ++d) acc = __fadd_rn(acc, __fmul_rn(ld<KT>(k, d, g, i), ld<float>(q, d, h, j)));
+  for (int64_t d = 0; d < dim; ++d) acc = acc + ld<KT>(k, d, g, i) * ld<float>(q, d, h, j);
   at(dst, i, j, h) = acc;
 }
 
 // One wave per (token j, head h) row: causal scaled softmax over keys
 // [0, min(n_past + j + 1, n_kv)), zeros beyond.
 __global__ void softmax_node_kernel(NodeView dst, NodeView src, int n_past, float scale) {
+#pragma clang fp contract(off)
   const int64_t n_kv = src.ne[0], n_tok = src.ne[1];
   const int64_t row = blockIdx.x;
   const int64_t j = row % n_tok, h = row / n_tok;
   const int64_t visible = min((int64_t)n_past + j + 1, n_kv);
   const int lane = threadIdx.x;
   float mx = -INFINITY;
-  for (int64_t i = lane; i < visible; i += kWave) mx = fmaxf(mx, __fmul_rn(ld<float>(src, i, j, h), scale));
+  for (int64_t i = lane; i < visible; i += kWave) mx = fmaxf(mx, ld<float>(src, i, j, h) * scale);
   mx = wave_max(mx);
   float sum = 0.f;
   for (int64_t i = lane; i < visible; i += kWave) {
-    const float e = expf(__fmul_rn(ld<float>(src, i, j, h), scale) - mx);
+    const float e = expf(ld<float>(src, i, j, h) * scale - mx);
     at(dst, i, j, h) = e;
     sum += e;
   }
   sum = wave_sum(sum);
-  const float inv = __fdiv_rn(1.f, sum);
-  for (int64_t i = lane; i < visible; i += kWave) at(dst, i, j, h) = __fmul_rn(at(dst, i, j, h), inv);
+  const float inv = 1.f / sum;
+  for (int64_t i = lane; i < visible; i += kWave) at(dst, i, j, h) = at(dst, i, j, h) * inv;
   for (int64_t i = visible + lane; i < n_kv; i += kWave) at(dst, i, j, h) = 0.f;
 }
 
 // dst [head_dim, n_head, n_tokens]: O[o,h,j] = sum_t V[o, h/n_rep, t] * P[t, j, h].
 template <typename VT>
 __global__ void attn_kqv_node_kernel(NodeView dst, NodeView probs, NodeView v, int n_rep) {
+#pragma clang fp contract(off)
   const int64_t dim = dst.ne[0], n_head = dst.ne[1], n_tok = dst.ne[2], n_kv = probs.ne[0];
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= dim * n_head * n_tok) return;
@@ -73,7 +77,7 @@ __global__ void attn_kqv_node_kernel(NodeView dst, NodeView probs, NodeView v, i
   const int64_t j = idx / (dim * n_head);
   const int64_t g = h / n_rep;
   float acc = 0.f;
-  for (int64_t t = 0; t < n_kv; ++t) acc = __fadd_rn(acc, __fmul_rn(ld<VT>(v, o, g, t), ld<float>(probs, t, j, h)));
+  for (int64_t t = 0; t < n_kv; ++t) acc = acc + ld<VT>(v, o, g, t) * ld<float>(probs, t, j, h);
   at(dst, o, h, j) = acc;
 }
 

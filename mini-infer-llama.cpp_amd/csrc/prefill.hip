@@ -1,14 +1,15 @@
 // prefill.hip -- fused causal ATTN_QK -> SOFTMAX -> ATTN_KQV for n_tokens > 1
 // queries (src/ops_cpu.cpp:304-410), on the FP32 matrix cores of gfx950.
 //
-// A wave owns one unit = (Q head h, block of 32 queries, chunk of C key
-// tiles of 32 keys); units never share LDS, so a workgroup's waves never
-// wait for each other. Per key tile the wave
-//   1. stages the 32 K and V rows of KV head h / n_rep into its own padded
-//      LDS tiles (coalesced 16-byte loads; F16 caches widen here);
+// One workgroup owns one (Q head h, block of 32 queries). Its waves take the
+// block's visible key tiles (32 keys each) round-robin; each wave keeps a
+// running (max, sum, O) per query and per tile
+//   1. writes the tile's 32 K and V rows of KV head h / n_rep, prefetched into
+//      registers during the previous tile, into its own padded LDS tiles
+//      (F16 caches widen on the way), and issues the loads of its next tile;
 //   2. computes S^T = K . Q^T (keys x queries) with D/2
-//      v_mfma_f32_32x32x2f32: A = K rows from LDS, B = the wave's queries,
-//      pre-scaled by scale*log2(e) and held in registers for the whole unit;
+//      v_mfma_f32_32x32x2f32: A = K rows from LDS, B = the block's queries,
+//      pre-scaled by scale*log2(e) and held in registers for the whole block;
 //   3. applies the causal mask (key > n_past + query) on tiles that reach the
 //      diagonal, and the online softmax: a lane holds 16 keys of one query and
 //      its partner lane (lane ^ 32) the other 16, so the row max is one
@@ -17,10 +18,11 @@
 //      probabilities S^T leave step 3 in exactly the B-operand layout of this
 //      product (register r of a lane = key 8(r/4) + 4(lane/32) + r%4), so no
 //      shuffle or LDS round trip is needed.
-// Queries whose visible keys span several chunks write (m, l, O) partials;
-// the last of those units to arrive (device-scope counter per head and
-// query block) merges them and resets the counter. Units are numbered from
-// the longest query block down, so long units start first.
+// The waves then merge their (m, l, O) through LDS with the stable rescaling
+// and write the block's output; nothing leaves the workgroup but the result.
+// Workgroups are numbered from the longest query block down so long blocks
+// start first, and the heads of one block are adjacent so K/V tiles of a
+// shared KV head are re-read from L2.
 #include "attn_common.h"
 #include "kernels.h"
 
@@ -39,44 +41,26 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
   constexpr int RPI = kWave / LPR;          // staging: rows per instruction
   constexpr int NLD = kPrefillKeys / RPI;   // staging: instructions per tile
   constexpr int WS = kPrefillKeys * (KS + VS);
-  constexpr int REC = kPrefillRows * (D + 2);
+  constexpr int RS = kPrefillRows * D + 2 * kPrefillRows;  // merge record
+  static_assert(RS <= WS, "merge record must fit the wave's staging area");
 
   extern __shared__ float lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int unit = blockIdx.x * (blockDim.x / kWave) + wave;
-  if (unit >= p.n_units) return;
-
+  const int nwaves = blockDim.x / kWave;
   float* kl = lds + wave * WS;
   float* vl = kl + kPrefillKeys * KS;
 
-  // unit -> (head h, query block i, key chunk j)
-  const int h = unit % p.n_head;
-  const int r = p.units_per_head - 1 - unit / p.n_head;
+  // workgroup -> (head h, query block i), longest blocks first
+  const int h = blockIdx.x % p.n_head;
+  const int i = p.n_qblocks - 1 - (int)(blockIdx.x / p.n_head);
   const int n_kv = p.n_past + p.n_tokens;
-  const int kt_all = (n_kv + kPrefillKeys - 1) / kPrefillKeys;
-  const int c0 = (p.n_past + kPrefillKeys - 1) / kPrefillKeys;
-  const int C = p.chunk_tiles;
-  const int64_t base = ceil_prefix(c0, C);
-  int lo_i = 0, hi_i = p.n_qblocks - 1;
-  while (lo_i < hi_i) {
-    const int mid = (lo_i + hi_i + 1) / 2;
-    if (ceil_prefix(c0 + mid, C) - base <= r)
-      lo_i = mid;
-    else
-      hi_i = mid - 1;
-  }
-  const int i = lo_i;
-  const int64_t f_i = ceil_prefix(c0 + i, C) - base;
-  const int j = r - (int)f_i;
-  const int kt_i = min(c0 + i + 1, kt_all);
-  const int nch = (kt_i + C - 1) / C;
-  const int t0 = j * C, t1 = min(t0 + C, kt_i);
+  const int q_first = i * kPrefillRows;
+  const int kt_i = (min(n_kv, p.n_past + q_first + kPrefillRows) + kPrefillKeys - 1) / kPrefillKeys;
 
   const int g = h / p.n_rep;
   const int col = lane & 31;  // query row in B / key row in A
   const int kh = lane >> 5;
-  const int q_first = i * kPrefillRows;
   const int qloc = q_first + col;
   const bool qvalid = qloc < p.n_tokens;
   const int qabs = p.n_past + qloc;
@@ -108,10 +92,11 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
   const int sr = lane / LPR, sc4 = lane % LPR;
   const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
 
-  for (int kt = t0; kt < t1; ++kt) {
+  // K/V rows of tile kt into registers (rows past n_kv read as zero).
+  float4 kr[NLD], vr[NLD];
+  auto fetch = [&](int kt) {
     const int key0 = kt * kPrefillKeys;
     const int kvalid = min(kPrefillKeys, n_kv - key0);
-    float4 kr[NLD], vr[NLD];
 #pragma unroll
     for (int li = 0; li < NLD; ++li) {
       const int row = li * RPI + sr;
@@ -119,6 +104,11 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
       kr[li] = ok ? load4<KT>(kb + (int64_t)(key0 + row) * p.k_s2 + sc4 * 4 * ELT) : zero4;
       vr[li] = ok ? load4<KT>(vb + (int64_t)(key0 + row) * p.v_s2 + sc4 * 4 * ELT) : zero4;
     }
+  };
+
+  if (wave < kt_i) fetch(wave);
+  for (int kt = wave; kt < kt_i; kt += nwaves) {
+    const int key0 = kt * kPrefillKeys;
     wave_lds_fence();
 #pragma unroll
     for (int li = 0; li < NLD; ++li) {
@@ -127,6 +117,7 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
       *reinterpret_cast<float4*>(&vl[row * VS + sc4 * 4]) = vr[li];
     }
     wave_lds_fence();
+    if (kt + nwaves < kt_i) fetch(kt + nwaves);  // in flight during this tile
 
     // S^T = K . Q^T
     floatx16 s = (floatx16)(0.f);
@@ -178,29 +169,12 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
       for (int db = 0; db < NDB; ++db)
         o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[db * 32], s[t], o[db], 0, 0, 0);
     }
-    wave_lds_fence();
   }
 
+  // Merge the waves through LDS: record = [32 rows][D] O, m[32], l[32].
   const float ltot = lsum + __shfl_xor(lsum, 32, kWave);
-
-  if (nch == 1) {
-    if (qvalid) {
-      const float inv = 1.f / ltot;
-      float* op = reinterpret_cast<float*>(reinterpret_cast<char*>(p.out) +
-                                           (int64_t)qloc * p.o_s2 + (int64_t)h * p.o_s1);
-#pragma unroll
-      for (int db = 0; db < NDB; ++db)
-#pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4)
-          *reinterpret_cast<float4*>(op + 32 * db + 8 * r4 + 4 * kh) =
-              make_float4(o[db][4 * r4 + 0] * inv, o[db][4 * r4 + 1] * inv,
-                          o[db][4 * r4 + 2] * inv, o[db][4 * r4 + 3] * inv);
-    }
-    return;
-  }
-
-  // Partial of this chunk: [32 rows][D] unnormalised O, then m[32], l[32].
-  float* rec = p.part + ((f_i + j) * p.n_head + h) * REC;
+  wave_lds_fence();
+  float* rec = kl;
 #pragma unroll
   for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -211,47 +185,23 @@ __global__ __launch_bounds__(kPrefillWaves* kWave) void prefill_kernel(const Pre
     rec[kPrefillRows * D + col] = m;
     rec[kPrefillRows * D + kPrefillRows + col] = ltot;
   }
-  __threadfence();
-  unsigned prev = 0;
-  if (lane == 0) prev = atomicAdd(&p.counter[h * p.n_qblocks + i], 1u);
-  prev = __shfl(prev, 0, kWave);
-  if (prev != (unsigned)(nch - 1)) return;
-  __threadfence();
-
-  // Last chunk to arrive: merge the nch partials of (h, i).
-  float mx = -INFINITY;
-  for (int jj = 0; jj < nch; ++jj) {
-    const float* rj = p.part + ((f_i + jj) * p.n_head + h) * REC;
-    mx = fmaxf(mx, rj[kPrefillRows * D + col]);
-  }
-  float acc[HALF];
-#pragma unroll
-  for (int d = 0; d < HALF; ++d) acc[d] = 0.f;
-  float total = 0.f;
-  for (int jj = 0; jj < nch; ++jj) {
-    const float* rj = p.part + ((f_i + jj) * p.n_head + h) * REC;
-    const float w = fast_exp2(rj[kPrefillRows * D + col] - mx);
-    total += w * rj[kPrefillRows * D + kPrefillRows + col];
-#pragma unroll
-    for (int d = 0; d < HALF; d += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(rj + col * D + kh * HALF + d);
-      acc[d + 0] += w * a.x;
-      acc[d + 1] += w * a.y;
-      acc[d + 2] += w * a.z;
-      acc[d + 3] += w * a.w;
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < kPrefillRows * D; idx += blockDim.x) {
+    const int row = idx / D, d = idx % D;
+    if (q_first + row >= p.n_tokens) continue;
+    float mx = -INFINITY;
+    for (int w = 0; w < nwaves; ++w) mx = fmaxf(mx, lds[w * WS + kPrefillRows * D + row]);
+    float a = 0.f, l = 0.f;
+    for (int w = 0; w < nwaves; ++w) {
+      const float* r = lds + w * WS;
+      const float wt = fast_exp2(r[kPrefillRows * D + row] - mx);  // idle wave: -inf -> 0
+      a += wt * r[row * D + d];
+      l += wt * r[kPrefillRows * D + kPrefillRows + row];
     }
-  }
-  if (qvalid) {
-    const float inv = 1.f / total;
     float* op = reinterpret_cast<float*>(reinterpret_cast<char*>(p.out) +
-                                         (int64_t)qloc * p.o_s2 + (int64_t)h * p.o_s1) +
-                kh * HALF;
-#pragma unroll
-    for (int d = 0; d < HALF; d += 4)
-      *reinterpret_cast<float4*>(op + d) =
-          make_float4(acc[d] * inv, acc[d + 1] * inv, acc[d + 2] * inv, acc[d + 3] * inv);
+                                         (int64_t)(q_first + row) * p.o_s2 + (int64_t)h * p.o_s1);
+    op[d] = a / l;
   }
-  if (lane == 0) p.counter[h * p.n_qblocks + i] = 0u;
 }
 
 template <int D, typename KT>
@@ -262,13 +212,10 @@ static hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
       hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<D, KT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
-  const unsigned blocks = (unsigned)((p.n_units + kPrefillWaves - 1) / kPrefillWaves);
-  hipLaunchKernelGGL((prefill_kernel<D, KT>), dim3(blocks), dim3(kPrefillWaves * kWave), lds,
-                     stream, p);
+  hipLaunchKernelGGL((prefill_kernel<D, KT>), dim3((unsigned)(p.n_head * p.n_qblocks)),
+                     dim3(kPrefillWaves * kWave), lds, stream, p);
   return hipGetLastError();
 }
-
-size_t prefill_record_floats(int head_dim) { return (size_t)kPrefillRows * (head_dim + 2); }
 
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, hipStream_t stream) {
   if (head_dim == 64)

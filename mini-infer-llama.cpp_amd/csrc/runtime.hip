@@ -57,14 +57,12 @@ struct State {
   bool ready = false;
   std::atomic<uint64_t> n_malloc{0}, n_free{0}, live{0}, peak{0};
   std::atomic<uint64_t> limit{0};
-  // Shared split/merge workspace: [counters][partials]; zeroed on allocation,
-  // the kernels leave every counter at zero when they finish.
+  // Shared split/merge workspace (partial records of the decode splits and
+  // of split prefill query blocks), grown on demand, never shrunk.
   char* ws = nullptr;
   size_t ws_bytes = 0;
 };
 State g;
-
-constexpr size_t kCounterBytes = 1 << 20;  // 256 Ki counters
 
 int dev_alloc(void** p, size_t bytes, const char* what) {
   const uint64_t lim = g.limit.load();
@@ -98,7 +96,7 @@ int bind_device() {
 // Grows the workspace to at least `bytes` of partials. Growth synchronises the
 // device first, so no in-flight kernel still uses the old buffer.
 int ensure_workspace(size_t part_bytes) {
-  const size_t need = kCounterBytes + ((part_bytes + 255) & ~size_t(255));
+  const size_t need = std::max<size_t>(256, (part_bytes + 255) & ~size_t(255));
   std::lock_guard<std::mutex> lk(g.mu);
   if (g.ws && g.ws_bytes >= need) return MI_HIP_OK;
   if (g.ws) {
@@ -110,18 +108,12 @@ int ensure_workspace(size_t part_bytes) {
   void* p = nullptr;
   int rc = dev_alloc(&p, need, "workspace");
   if (rc) return rc;
-  hipError_t e = hipMemset(p, 0, need);
-  if (e != hipSuccess) {
-    dev_free(p, need);
-    return hip_fail(e, "hipMemset(workspace)");
-  }
   g.ws = static_cast<char*>(p);
   g.ws_bytes = need;
   return MI_HIP_OK;
 }
 
-unsigned* ws_counters() { return reinterpret_cast<unsigned*>(g.ws); }
-float* ws_part() { return reinterpret_cast<float*>(g.ws + kCounterBytes); }
+float* ws_part() { return reinterpret_cast<float*>(g.ws); }
 
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
@@ -134,52 +126,30 @@ int env_int(const char* name, int dflt) {
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodePlan {
-  int group = 1, n_chunks = 1, splits = 1;
-  size_t part_floats = 0, counters = 0;
+  int group = 1, n_chunks = 1, splits = 1, waves = 1;
+  size_t part_floats = 0;
 };
 
 // Splits per (item, head chunk) so the launch has about `target` workgroups,
-// at most one 64-position tile per split.
+// each split at least one 64-position tile; one wave per tile of a split up
+// to kDecodeWaves.
 DecodePlan plan_decode(int n_items, int n_head_kv, int n_rep, int head_dim, int max_n_kv) {
   DecodePlan p;
   p.group = mi::decode_group_size(n_rep);
   p.n_chunks = n_rep / p.group;
   const int groups = n_items * n_head_kv * p.n_chunks;
-  const int target = std::max(1, env_int("MI_HIP_DECODE_WGS", 1024));
-  const int max_splits = std::max(1, (max_n_kv + mi::kDecodeTile - 1) / mi::kDecodeTile);
+  const int target = std::max(1, env_int("MI_HIP_DECODE_WGS", 256));
+  // at least one tile per wave of a full workgroup when the grid is small
+  const int max_splits =
+      std::max(1, (max_n_kv + mi::kDecodeTile * mi::kDecodeWaves - 1) / (mi::kDecodeTile * mi::kDecodeWaves));
   int s = (target + groups - 1) / groups;
   const int forced = env_int("MI_HIP_DECODE_SPLITS", 0);
   if (forced > 0) s = forced;
   p.splits = std::max(1, std::min(s, max_splits));
-  p.counters = (size_t)groups;
+  // one wave per 64-position tile of a split, up to kDecodeWaves
+  const int per_split = ((max_n_kv + p.splits - 1) / p.splits + mi::kDecodeTile - 1) / mi::kDecodeTile;
+  p.waves = std::max(1, std::min(mi::kDecodeWaves, per_split));
   p.part_floats = p.splits > 1 ? (size_t)groups * p.splits * mi::decode_record_floats(head_dim, p.group) : 0;
-  return p;
-}
-
-struct PrefillPlan {
-  int chunk = 1, n_qblocks = 1, units_per_head = 1, n_units = 1;
-  size_t part_floats = 0, counters = 0;
-};
-
-PrefillPlan plan_prefill(int n_head, int head_dim, int n_past, int n_tokens) {
-  PrefillPlan p;
-  const int kt_all = (n_past + n_tokens + 31) / 32;
-  const int c0 = (n_past + 31) / 32;
-  p.n_qblocks = (n_tokens + 31) / 32;
-  const int last = p.n_qblocks - 1;
-  const int kt_last = std::min(c0 + last + 1, kt_all);
-  // key tiles over all query blocks of one head
-  const int64_t tiles = (int64_t)(c0 + 1 + c0 + last) * last / 2 + kt_last;
-  const int target = std::max(1, env_int("MI_HIP_PREFILL_UNITS", 2048));
-  int64_t c = (tiles * n_head + target - 1) / target;
-  const int forced = env_int("MI_HIP_PREFILL_CHUNK", 0);
-  if (forced > 0) c = forced;
-  p.chunk = (int)std::max<int64_t>(1, std::min<int64_t>(c, kt_all));
-  p.units_per_head = (int)(mi::ceil_prefix(c0 + last, p.chunk) - mi::ceil_prefix(c0, p.chunk) +
-                           (kt_last + p.chunk - 1) / p.chunk);
-  p.n_units = p.units_per_head * n_head;
-  p.counters = (size_t)n_head * p.n_qblocks;
-  p.part_floats = (size_t)p.n_units * mi::prefill_record_floats(head_dim);
   return p;
 }
 
@@ -311,8 +281,6 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
   const int chunk_items = std::min(n, mi::kDecodeMaxItems);
   const DecodePlan plan =
       plan_decode(chunk_items, r0.n_head_kv, items[0].n_rep, r0.head_dim, max_n_kv);
-  if (plan.counters * sizeof(unsigned) > kCounterBytes)
-    return fail(MI_HIP_E_UNSUPPORTED, "too many head groups in one launch");
   rc = ensure_workspace(plan.part_floats * sizeof(float));
   if (rc) return rc;
   for (int base = 0; base < n; base += mi::kDecodeMaxItems) {
@@ -329,9 +297,9 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
     p.n_head_kv = r0.n_head_kv;
     p.n_chunks = plan.n_chunks;
     p.splits = plan.splits;
+    p.waves = plan.waves;
     p.scale_log2e = items[0].scale * kLog2e;
     p.part = ws_part();
-    p.counter = ws_counters();
     hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
   }
@@ -339,11 +307,6 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
 }
 
 int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream) {
-  const PrefillPlan plan = plan_prefill(a->n_head, r.head_dim, a->n_past, a->n_tokens);
-  if (plan.counters * sizeof(unsigned) > kCounterBytes)
-    return fail(MI_HIP_E_UNSUPPORTED, "too many query blocks in one launch");
-  int rc = ensure_workspace(plan.part_floats * sizeof(float));
-  if (rc) return rc;
   mi::PrefillParams p{};
   p.k = r.k;
   p.v = r.v;
@@ -361,28 +324,18 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   p.n_rep = a->n_rep;
   p.n_past = a->n_past;
   p.n_tokens = a->n_tokens;
-  p.chunk_tiles = plan.chunk;
-  p.n_qblocks = plan.n_qblocks;
-  p.units_per_head = plan.units_per_head;
-  p.n_units = plan.n_units;
+  p.n_qblocks = (a->n_tokens + mi::kPrefillRows - 1) / mi::kPrefillRows;
   p.scale_log2e = a->scale * kLog2e;
-  p.part = ws_part();
-  p.counter = ws_counters();
   hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, stream);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   return MI_HIP_OK;
 }
 
-// Workspace bytes that cover every decode and prefill call up to n_ctx.
+// Workspace bytes that cover every decode call up to n_ctx (prefill needs none).
 size_t workspace_for(const mi_hip_kv_desc& d) {
   const int n_rep = d.n_head / d.n_head_kv;
   const DecodePlan dp = plan_decode(1, d.n_head_kv, n_rep, d.head_dim, d.n_ctx);
-  size_t need = dp.part_floats;
-  for (int t : {d.n_ctx, std::max(2, d.n_ctx / 2)}) {
-    const PrefillPlan pp = plan_prefill(d.n_head, d.head_dim, 0, t);
-    need = std::max(need, pp.part_floats);
-  }
-  return need * sizeof(float);
+  return dp.part_floats * sizeof(float);
 }
 
 // ---------------------------------------------------------------------------
