@@ -37,7 +37,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: decode,prefill,d7b,perlayer")
+    ap.add_argument("--only", default="",
+                    help="comma list: decode,prefill,d7b,perlayer,copy (copy: the counter "
+                         "calibration workload, only when named)")
     return ap.parse_args()
 
 
@@ -155,6 +157,15 @@ def bench_prefill(torch, mh, lib, stream, steps, warmup, n, h=14, hkv=2, d=64):
                 tflops=flops / (kern_ms * 1e-3) / 1e12)
 
 
+def bench_copy(torch, steps, warmup, nbytes=256 << 20):
+    """A plain device-to-device copy of known size: the calibration workload for
+    the FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = nbytes)."""
+    src = torch.empty(nbytes // 4, device="cuda").uniform_()
+    dst = torch.empty_like(src)
+    ms, kern_ms = run_timed(torch, lambda i: dst.copy_(src), steps, warmup)
+    return dict(bytes=nbytes, kernel_ms=kern_ms, gbps=2 * nbytes / (kern_ms * 1e-3) / 1e9)
+
+
 def cpu_baseline(n_layers_sample=24, n_kv=4096):
     """The reference three-node CPU path on the host cores (bounded sample:
     24 layers' decode attention at n_kv = 4096, 1 warmup + 7 timed passes)."""
@@ -237,6 +248,11 @@ def main():
         res["per_layer"] = bench_decode_per_layer(torch, mh, lib, stream, args.steps, args.warmup)
         print(f"# per-layer launches: {res['per_layer']['us_per_layer']:.2f} us/layer",
               file=sys.stderr, flush=True)
+
+    if "copy" in only:
+        res["copy"] = bench_copy(torch, max(5, args.steps // 10), 2)
+        print(f"# copy 256 MiB: {res['copy']['gbps']:.1f} GB/s (read + write)", file=sys.stderr,
+              flush=True)
 
     cpu = None
     if not args.no_cpu:

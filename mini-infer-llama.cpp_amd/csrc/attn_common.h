@@ -13,9 +13,7 @@ constexpr int kWave = 64;
 // Decode (one query token against n_kv cached positions).
 // ---------------------------------------------------------------------------
 constexpr int kDecodeMaxItems = 32;  // items per launch (they ride in kernarg)
-constexpr int kDecodeTile = 64;      // positions per wave iteration (lane = position)
-constexpr int kDecodeKStride = 68;   // LDS floats per staged K row (64 + 4 pad)
-constexpr int kDecodeWaves = 4;      // waves per workgroup
+constexpr int kDecodeTile = 64;      // positions per tile (lane = position in QK)
 
 // One independent decode problem. Byte strides; the head_dim axis of K, V, Q
 // and O is contiguous.
@@ -29,19 +27,24 @@ struct DecodeItem {
   int64_t q_s1;        // Q: bytes between heads
   int64_t o_s1;        // O: bytes between heads
   int32_t n_kv;        // keys [0, n_kv) are visible
+  int32_t wave0;       // first wave (= workgroup) of this item
+  int32_t nw;          // waves per (KV head, head chunk) group
   int32_t pad_;
 };
 
+// Work decomposition: a "group" is (item, KV head g, head chunk hc), i.e. the
+// G Q heads g*n_rep + hc*G .. + G - 1 that read KV head g. Its ceil(n_kv/64)
+// position tiles are split into nw contiguous runs, one per wave; each wave is
+// one workgroup. Waves of an item are numbered group-major from wave0.
 struct DecodeParams {
   DecodeItem item[kDecodeMaxItems];
   int32_t n_items;
   int32_t n_rep;        // Q heads per KV head
   int32_t n_head_kv;
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
-  int32_t splits;       // position splits per (item, head chunk)
-  int32_t waves;        // waves per workgroup (1..kDecodeWaves)
+  int32_t n_waves;      // total waves (grid size)
   float scale_log2e;    // softmax scale * log2(e)
-  float* part;          // split records (splits > 1), merged by decode_merge_kernel
+  float* part;          // one (m, l, acc) record per wave when nw > 1
 };
 
 // ---------------------------------------------------------------------------
@@ -144,14 +147,6 @@ template <>
 __device__ inline float4 load4<_Float16>(const char* p) {
   const half4_t h = *reinterpret_cast<const half4_t*>(p);
   return make_float4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
-}
-
-// Uniform (scalar-cache) view of a global buffer: loads through it with a
-// wave-uniform address are issued as scalar loads into SGPRs.
-typedef const __attribute__((address_space(4))) float* const_f32_ptr;
-
-__device__ inline const_f32_ptr as_const(const float* p) {
-  return (const_f32_ptr)(p);
 }
 
 }  // namespace mi

@@ -1,28 +1,32 @@
 // decode.hip -- fused ATTN_QK -> causal SOFTMAX -> ATTN_KQV for one query
 // token (src/ops_cpu.cpp:304-410 with n_tokens == 1), HBM-bound, no MFMA.
 //
-// Work decomposition
-//   grid.y = (item, KV head g, head chunk): the G Q heads g*n_rep + hc*G ..
-//            + G - 1 that share KV head g (GQA is an index mapping: every
-//            K/V row is read once for all G heads, never copied).
-//   grid.x = split of the positions [0, n_kv) (split-KV); each workgroup's
-//            kDecodeWaves waves take interleaved 64-position tiles of its
-//            split and keep a running (max, sum, acc) per head.
-// The wave's G query vectors stay in registers for the whole kernel, spread
-// over the 16 lanes of each row. Per 64-position tile, one wave:
-//   1. requests the tile's K rows (coalesced 16-byte loads);
-//   2. stages K rows 64 dims at a time through a swizzled LDS tile and lets
-//      lane i own position i: each lane dots its row with the G queries, whose
-//      elements reach every lane as DPP row-broadcast FMA operands;
-//   3. requests the tile's V rows, updates the running max (DPP row
-//      reduction + readlane, no LDS),
-//      rescales, exponentiates (exp2 of log2e-prescaled scores) and writes
-//      the probabilities to LDS;
-//   4. accumulates P.V with lanes owning 4 output dims of one row.
-// Waves of a workgroup merge through LDS. With one split the workgroup writes
-// the output; otherwise it writes an (m, l, acc) record per head to the
-// workspace and decode_merge_kernel, launched next on the same stream,
-// combines the splits with the stable rescaling
+// Work decomposition. A group is (item, KV head g, head chunk hc): the G Q
+// heads g*n_rep + hc*G .. + G - 1 that read KV head g (GQA is an index
+// mapping: every K/V row is read once for all G heads, never copied). A
+// group's positions form ceil(n_kv / 64) tiles, split into nw contiguous runs,
+// one per wave; each wave is a workgroup of its own. The host sizes nw so the
+// launch has about one wave per SIMD and every run has the same number of
+// tiles to within one.
+//
+// Per wave: the G query vectors stay in registers, spread over the 16 lanes of
+// each row. The K and V tiles of NBUF tiles are requested up front and each
+// slot is refilled as soon as its registers are free, so every wave keeps one
+// to two tiles of HBM requests in flight while it computes. Loads go through
+// buffer resources bounded by the group's last row: rows past n_kv read as
+// zero without a memory request, and so do refills past the run's end (a
+// zero-sized resource), which keeps the loop free of branches around loads.
+// Per tile:
+//   1. K rows go to a swizzled LDS tile and lane i takes position i: each
+//      lane dots its row with the G queries, whose elements reach every lane
+//      as DPP row-broadcast FMA operands (no memory round trip);
+//   2. online softmax in base 2: running max by DPP row reduction + readlane,
+//      exp2 of log2e-prescaled scores; probabilities to LDS;
+//   3. P.V with lanes owning 4 output dims of one row, V straight from the
+//      registers it was loaded into.
+// A run that covers its whole group writes O; otherwise the wave writes an
+// (m, l, acc) record and decode_merge_kernel, launched next on the same
+// stream, combines the nw records of each group with the stable rescaling
 // O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s.
 // (No cross-workgroup signalling inside a kernel: on this part a device-scope
 // fence writes back and invalidates the whole L2 of the XCD.)
@@ -33,45 +37,144 @@
 
 namespace mi {
 
-template <int D, typename KT, int G>
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw (unswizzled, stride 0) buffer descriptor word 3 of the gfx9 family.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// Descriptor over [p, p + bytes): loads at offsets >= bytes return zero and
+// make no memory request.
+__device__ inline rsrc_t make_rsrc(const char* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, (int)bytes,
+                                           kRawBufferWord3);
+}
+
+// Four consecutive cache elements, held in registers at storage width.
+template <typename KT>
+struct Cache;
+template <>
+struct Cache<float> {
+  typedef f32x4 raw;
+  static __device__ inline raw load(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+  }
+  static __device__ inline float4 widen(raw x) { return make_float4(x.x, x.y, x.z, x.w); }
+};
+template <>
+struct Cache<_Float16> {
+  typedef half4_t raw;
+  static __device__ inline raw load(rsrc_t r, unsigned off) {
+    return __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+  }
+  static __device__ inline float4 widen(raw h) {
+    return make_float4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
+  }
+};
+
+// Record of one wave's run: m[G], l[G] (padded to 4), then acc[G][D].
+__host__ __device__ constexpr int record_header(int g) { return (2 * g + 3) & ~3; }
+
+// s[J % NACC][h] += bcast_J(q[h]) * k for all heads; heads are interleaved so
+// the DPP operand of an instruction was written at least two instructions
+// earlier (no hazard wait states).
+template <int J, int G, int NACC>
+__device__ __forceinline__ void qk_step(float (&s)[NACC][G], const float (&q)[G], float k) {
+#pragma unroll
+  for (int h = 0; h < G; ++h) s[J % NACC][h] = fmac_bcast<J>(s[J % NACC][h], q[h], k);
+}
+
+// DEPTH: tiles of K/V requested ahead per wave. Depth 1 keeps the wave within
+// 256 registers, so each SIMD runs two waves and one computes while the other
+// waits on memory; depth 2 holds two tiles (one wave per SIMD).
+template <int D, typename KT, int G, int DEPTH>
 __device__ __forceinline__ void decode_body(const DecodeParams& p) {
+  typedef Cache<KT> C;
+  typedef typename C::raw raw_t;
   constexpr int ELT = (int)sizeof(KT);
-  constexpr int NCH = D / 64;                    // 64-dim chunks staged for QK
-  constexpr int LPR = D / 4;                     // PV: lanes per cache row
-  constexpr int RPI = kWave / LPR;               // PV: rows per load instruction
-  constexpr int NV = kDecodeTile / RPI;          // PV: load instructions per tile
-  constexpr int TS = kDecodeTile * 64;  // LDS floats per wave (swizzled, unpadded)
-  constexpr int HDR = (2 * G + 3) & ~3;          // record header: m[G], l[G]
-  constexpr int REC = HDR + G * D;               // one merge record
+  constexpr int NCH = D / 64;                 // 64-dim K chunks per row
+  constexpr int NK = NCH * 16;                // K loads per lane per tile
+  constexpr int LPR = D / 4;                  // PV: lanes per V row
+  constexpr int RPI = kWave / LPR;            // PV: rows per load
+  constexpr int NV = kDecodeTile / RPI;       // V loads per lane per tile
+  constexpr int NBUF = DEPTH;
+  constexpr int NACC = G >= 3 ? 1 : (G == 2 ? 2 : 3);
+  constexpr int HDR = record_header(G);
+  constexpr int REC = HDR + G * D;
+  constexpr int CS = kDecodeTile * 64;        // LDS floats per staged K chunk
 
-  extern __shared__ float lds[];
+  __shared__ float klds[NCH * CS];  // the K tile (F32, swizzled), then P
 
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int nwaves = blockDim.x / kWave;
+  const int lane = threadIdx.x;
+  const int wid = blockIdx.x;
 
-  const int split = blockIdx.x;
-  const int grp = blockIdx.y;
-  const int per_item = p.n_head_kv * p.n_chunks;
-  const int it_idx = grp / per_item;
-  const int g = (grp % per_item) / p.n_chunks;
-  const int hc = grp % p.n_chunks;
-  const DecodeItem& it = p.item[it_idx];
-
-  const int n_kv = it.n_kv;
-  const int per_split =
-      ((n_kv + p.splits - 1) / p.splits + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
-  const int lo = split * per_split;
-  const int hi = min(n_kv, lo + per_split);
+  // item, group and run of this wave (items are few: a scalar scan)
+  int ii = 0;
+  while (ii + 1 < p.n_items && wid >= p.item[ii + 1].wave0) ++ii;
+  const DecodeItem& it = p.item[ii];
+  const int local = wid - it.wave0;
+  const int gl = local / it.nw;
+  const int run = local - gl * it.nw;
+  const int g = gl / p.n_chunks;
+  const int hc = gl - g * p.n_chunks;
   const int head0 = g * p.n_rep + hc * G;
+  const int n_kv = it.n_kv;
+  const int tpg = (n_kv + kDecodeTile - 1) / kDecodeTile;
+  const int t_begin = (int)((int64_t)tpg * run / it.nw);
+  const int t_end = (int)((int64_t)tpg * (run + 1) / it.nw);
 
-  const char* kbase = it.k + (int64_t)g * it.k_s1;
-  const char* vbase = it.v + (int64_t)g * it.v_s1;
-  const float* q0 = reinterpret_cast<const float*>(reinterpret_cast<const char*>(it.q) +
-                                                   (int64_t)head0 * it.q_s1);
-  const int64_t q_s1f = it.q_s1 / 4;
+  // Offsets are 32-bit (the host checks n_kv * stride < 2^31).
+  const int ks2 = (int)it.k_s2, vs2 = (int)it.v_s2;
+  const rsrc_t kres = make_rsrc(it.k + (int64_t)g * it.k_s1, (unsigned)((n_kv - 1) * ks2 + D * ELT));
+  const rsrc_t vres = make_rsrc(it.v + (int64_t)g * it.v_s1, (unsigned)((n_kv - 1) * vs2 + D * ELT));
+  const rsrc_t none = make_rsrc(it.k, 0u);
 
-  float* klds = lds + wave * TS;
+  const int kr = lane >> 4, kc = lane & 15;    // K staging: 16 lanes per 64-dim chunk row
+  const int vr = lane / LPR, vc = lane % LPR;  // PV: LPR lanes per V row
+  const unsigned klane = (unsigned)(kr * ks2 + kc * 4 * ELT);
+  const unsigned vlane = (unsigned)(vr * vs2 + vc * 4 * ELT);
+
+  // The G query vectors, requested before any cache tile:
+  // qv[h][c] = Q[head0 + h][16 c + (lane & 15)].
+  float qv[G][D / 16];
+  {
+    const float* q0 = reinterpret_cast<const float*>(reinterpret_cast<const char*>(it.q) +
+                                                     (int64_t)head0 * it.q_s1);
+    const int64_t q_s1f = it.q_s1 / 4;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) qv[h][c] = q0[h * q_s1f + 16 * c + (lane & 15)];
+  }
+
+  raw_t kb[NBUF][NK], vb[NBUF][NV];
+  // (the lane's base offset passes through an empty asm at every issue so the
+  // per-load offsets are formed next to their loads instead of being hoisted
+  // out of the loop, which would hold one register per load)
+  auto issue_k = [&](raw_t (&dst)[NK], int t) __attribute__((always_inline)) {
+    const rsrc_t r = t < t_end ? kres : none;
+    unsigned base = klane;
+    asm volatile("" : "+v"(base));
+    base += (unsigned)(t * kDecodeTile * ks2);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        dst[c * 16 + i] = C::load(r, base + (unsigned)(i * 4 * ks2 + c * 64 * ELT));
+  };
+  auto issue_v = [&](raw_t (&dst)[NV], int t) __attribute__((always_inline)) {
+    const rsrc_t r = t < t_end ? vres : none;
+    unsigned base = vlane;
+    asm volatile("" : "+v"(base));
+    base += (unsigned)(t * kDecodeTile * vs2);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) dst[i] = C::load(r, base + (unsigned)(i * RPI * vs2));
+  };
+#pragma unroll
+  for (int b = 0; b < NBUF; ++b) {
+    issue_k(kb[b], t_begin + b);
+    issue_v(vb[b], t_begin + b);
+  }
 
   float m[G], l[G], acc[G][4];
 #pragma unroll
@@ -82,112 +185,77 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
   }
 
-  const int kr = lane >> 4, kc = lane & 15;    // K staging: 16 lanes per 64-dim row
-  const int vr = lane / LPR, vc = lane % LPR;  // PV: LPR lanes per row
-  // Strides fit 32 bits (checked by the host: 64 rows of any stride < 2^31).
-  const int ks2 = (int)it.k_s2, vs2 = (int)it.v_s2;
-  const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto process = [&](raw_t (&kt)[NK], raw_t (&vt)[NV], int t) __attribute__((always_inline)) {
+    const int nvalid = min(kDecodeTile, n_kv - t * kDecodeTile);
 
-  // The G query vectors, spread over the 16 lanes of every row:
-  // qv[h][c] = Q[head0 + h][16 c + (lane & 15)]. A DPP row broadcast hands
-  // dim 16 c + j to every lane as an FMA operand: no memory round trip.
-  float qv[G][D / 16];
+    // K tile to LDS: chunk c of row r is 256 contiguous bytes whose 16-byte
+    // slot s holds dims 64c + 4 (s ^ (r & 15)) .. +3, so lane r reading slot
+    // d of its own row hits 16 distinct bank groups across 16 lanes.
+    wave_lds_fence();
 #pragma unroll
-  for (int h = 0; h < G; ++h)
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) qv[h][c] = q0[h * q_s1f + 16 * c + (lane & 15)];
-
-  for (int p0 = lo + wave * kDecodeTile; p0 < hi; p0 += nwaves * kDecodeTile) {
-    const int nvalid = min(kDecodeTile, hi - p0);
-    const int last = nvalid - 1;
-    const char* ktile = kbase + (int64_t)p0 * it.k_s2;  // wave-uniform
-    const char* vtile = vbase + (int64_t)p0 * it.v_s2;
-
-    float s[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) s[h] = 0.f;
-    float4 vreg[NV];
-
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      // Rows p0..p0+63, dims [64c, 64c+64) of KV head g: row r is 256
-      // contiguous LDS bytes whose 16-byte slot s holds chunk s ^ (r & 15),
-      // so lane r reading chunk d of its own row hits 16 distinct bank groups
-      // across 16 lanes. Rows past the split end re-read its last row (their
-      // scores are masked).
-      float4 kreg[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const unsigned off = (unsigned)(min(i * 4 + kr, last) * ks2 + (c * 64 + kc * 4) * ELT);
-        kreg[i] = load4<KT>(ktile + off);
-      }
-      wave_lds_fence();
+    for (int c = 0; c < NCH; ++c)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int row = i * 4 + kr;
-        *reinterpret_cast<float4*>(&klds[row * 64 + ((kc ^ (row & 15)) * 4)]) = kreg[i];
+        *reinterpret_cast<float4*>(&klds[c * CS + row * 64 + ((kc ^ (row & 15)) * 4)]) =
+            C::widen(kt[c * 16 + i]);
       }
-      wave_lds_fence();
+    wave_lds_fence();
+    issue_k(kt, t + NBUF);  // the slot's K registers are free again
 
-      // Lane = position: dot its row with the G queries. (qv passes through an
-      // empty asm so the broadcasts stay here instead of being hoisted out of
-      // the tile loop, which would need one register per broadcast value.)
+    float s[NACC][G];
+#pragma unroll
+    for (int a = 0; a < NACC; ++a)
+#pragma unroll
+      for (int h = 0; h < G; ++h) s[a][h] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const float* krow = klds + c * CS + lane * 64;
 #pragma unroll
       for (int q16 = 0; q16 < 4; ++q16) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) asm volatile("" : "+v"(qv[h][c * 4 + q16]));
-        const float4 k0 = *reinterpret_cast<const float4*>(
-            &klds[lane * 64 + (((4 * q16 + 0) ^ (lane & 15)) * 4)]);
-        const float4 k1 = *reinterpret_cast<const float4*>(
-            &klds[lane * 64 + (((4 * q16 + 1) ^ (lane & 15)) * 4)]);
-        const float4 k2 = *reinterpret_cast<const float4*>(
-            &klds[lane * 64 + (((4 * q16 + 2) ^ (lane & 15)) * 4)]);
-        const float4 k3 = *reinterpret_cast<const float4*>(
-            &klds[lane * 64 + (((4 * q16 + 3) ^ (lane & 15)) * 4)]);
+        // (qv passes through an empty asm so the broadcasts stay here instead
+        // of being hoisted out of the tile loop, which would need one
+        // register per broadcast value)
+        float qq[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          const float qq = qv[h][c * 4 + q16];
-          float a = s[h];
-          a = fmac_bcast<0>(a, qq, k0.x);
-          a = fmac_bcast<1>(a, qq, k0.y);
-          a = fmac_bcast<2>(a, qq, k0.z);
-          a = fmac_bcast<3>(a, qq, k0.w);
-          a = fmac_bcast<4>(a, qq, k1.x);
-          a = fmac_bcast<5>(a, qq, k1.y);
-          a = fmac_bcast<6>(a, qq, k1.z);
-          a = fmac_bcast<7>(a, qq, k1.w);
-          a = fmac_bcast<8>(a, qq, k2.x);
-          a = fmac_bcast<9>(a, qq, k2.y);
-          a = fmac_bcast<10>(a, qq, k2.z);
-          a = fmac_bcast<11>(a, qq, k2.w);
-          a = fmac_bcast<12>(a, qq, k3.x);
-          a = fmac_bcast<13>(a, qq, k3.y);
-          a = fmac_bcast<14>(a, qq, k3.z);
-          a = fmac_bcast<15>(a, qq, k3.w);
-          s[h] = a;
+          asm volatile("" : "+v"(qv[h][c * 4 + q16]));
+          qq[h] = qv[h][c * 4 + q16];
         }
+        const float4 k0 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 0) ^ (lane & 15)) * 4]);
+        const float4 k1 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 1) ^ (lane & 15)) * 4]);
+        const float4 k2 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 2) ^ (lane & 15)) * 4]);
+        const float4 k3 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 3) ^ (lane & 15)) * 4]);
+        qk_step<0>(s, qq, k0.x);
+        qk_step<1>(s, qq, k0.y);
+        qk_step<2>(s, qq, k0.z);
+        qk_step<3>(s, qq, k0.w);
+        qk_step<4>(s, qq, k1.x);
+        qk_step<5>(s, qq, k1.y);
+        qk_step<6>(s, qq, k1.z);
+        qk_step<7>(s, qq, k1.w);
+        qk_step<8>(s, qq, k2.x);
+        qk_step<9>(s, qq, k2.y);
+        qk_step<10>(s, qq, k2.z);
+        qk_step<11>(s, qq, k2.w);
+        qk_step<12>(s, qq, k3.x);
+        qk_step<13>(s, qq, k3.y);
+        qk_step<14>(s, qq, k3.z);
+        qk_step<15>(s, qq, k3.w);
       }
     }
 
-    // V rows of the tile (requested after QK so that the V and K register
-    // sets never coexist; other waves cover the latency).
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int row = i * RPI + vr;
-      const unsigned off = (unsigned)(min(row, last) * vs2 + vc * 4 * ELT);
-      const float4 x = load4<KT>(vtile + off);
-      vreg[i] = row < nvalid ? x : zero4;
-    }
-
-    // Online softmax: wave-uniform running max per head (DPP + readlane),
-    // per-lane partial sums.
+    // Online softmax: wave-uniform running max per head, per-lane sums.
     const bool valid = lane < nvalid;
     float pv[8];
 #pragma unroll
     for (int h = 0; h < 8; ++h) pv[h] = 0.f;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float x = valid ? s[h] * p.scale_log2e : -INFINITY;
+      float sh = s[0][h];
+#pragma unroll
+      for (int a = 1; a < NACC; ++a) sh += s[a][h];
+      const float x = valid ? sh * p.scale_log2e : -INFINITY;
       const float mn = fmaxf(m[h], wave_max_dpp(x));
       const float alpha = fast_exp2(m[h] - mn);
       const float e = fast_exp2(x - mn);
@@ -205,14 +273,15 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
       *reinterpret_cast<float4*>(&klds[lane * 8 + 4]) = make_float4(pv[4], pv[5], pv[6], pv[7]);
     wave_lds_fence();
 
+    // O += P.V (rows past n_kv loaded as zero and have P = 0).
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int row = i * RPI + vr;
       const float4 pa = *reinterpret_cast<const float4*>(&klds[row * 8]);
-      float4 pb = zero4;
+      float4 pb = make_float4(0.f, 0.f, 0.f, 0.f);
       if (G > 4) pb = *reinterpret_cast<const float4*>(&klds[row * 8 + 4]);
       const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      const float4 vv = vreg[i];
+      const float4 vv = C::widen(vt[i]);
 #pragma unroll
       for (int h = 0; h < G; ++h) {
         acc[h][0] = fmaf(pr[h], vv.x, acc[h][0]);
@@ -221,7 +290,19 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
         acc[h][3] = fmaf(pr[h], vv.w, acc[h][3]);
       }
     }
-    wave_lds_fence();
+    issue_v(vt, t + NBUF);
+  };
+
+  // Slots are used in turn; exits leave the loop rather than re-entering it,
+  // so the wait counts at the loop head see one pattern of loads in flight.
+  int t = t_begin;
+  while (true) {
+    process(kb[0], vb[0], t);
+    if (++t >= t_end) break;
+    if (NBUF > 1) {
+      process(kb[NBUF - 1], vb[NBUF - 1], t);
+      if (++t >= t_end) break;
+    }
   }
 
   // Wave totals: l over all lanes, acc over the RPI lanes sharing a column.
@@ -235,9 +316,20 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
     }
   }
 
-  // Workgroup merge through LDS.
-  __syncthreads();
-  float* rec = lds + wave * REC;
+  if (it.nw == 1) {  // the run is the whole group
+    if (lane < LPR) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        const float inv = 1.f / l[h];
+        float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) +
+                                            (int64_t)(head0 + h) * it.o_s1);
+        *reinterpret_cast<float4*>(o + 4 * lane) =
+            make_float4(acc[h][0] * inv, acc[h][1] * inv, acc[h][2] * inv, acc[h][3] * inv);
+      }
+    }
+    return;
+  }
+  float* rec = p.part + (int64_t)wid * REC;
   if (lane == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -251,143 +343,120 @@ __device__ __forceinline__ void decode_body(const DecodeParams& p) {
       *reinterpret_cast<float4*>(&rec[HDR + h * D + 4 * lane]) =
           make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
   }
-  __syncthreads();
-
-  const bool direct = p.splits == 1;
-  float* prec = p.part + ((int64_t)grp * p.splits + split) * REC;
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int h = idx / D, d = idx % D;
-    float mx = -INFINITY;
-    for (int w = 0; w < nwaves; ++w) mx = fmaxf(mx, lds[w * REC + h]);
-    float a = 0.f, sum = 0.f;
-    if (mx > -INFINITY) {
-      for (int w = 0; w < nwaves; ++w) {
-        const float sc = fast_exp2(lds[w * REC + h] - mx);
-        a += sc * lds[w * REC + HDR + h * D + d];
-        sum += sc * lds[w * REC + G + h];
-      }
-    }
-    if (direct) {
-      float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) +
-                                          (int64_t)(head0 + h) * it.o_s1);
-      o[d] = a / sum;
-    } else {
-      prec[HDR + h * D + d] = a;
-      if (d == 0) {
-        prec[h] = mx;
-        prec[G + h] = sum;
-      }
-    }
-  }
 }
 
-// Two occupancy variants of the same body: two waves per SIMD (register
-// budget 256) or one (512).
 template <int D, typename KT, int G>
-__global__ __launch_bounds__(kDecodeWaves* kWave) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(const DecodeParams p) {
-  decode_body<D, KT, G>(p);
+  decode_body<D, KT, G, 1>(p);
 }
 
 template <int D, typename KT, int G>
-__global__ __launch_bounds__(kDecodeWaves* kWave) void decode_kernel_wide(const DecodeParams p) {
-  decode_body<D, KT, G>(p);
+__global__ __launch_bounds__(kWave) void decode_kernel_deep(const DecodeParams p) {
+  decode_body<D, KT, G, 2>(p);
 }
 
-// Combines the split records of one (item, head chunk) per workgroup in two
-// passes: per head the max m over splits, the weights w_s = 2^(m_s - m) and
-// the denominator; then every (head, dim) output is an independent weighted
-// sum over the splits' unnormalised accumulators.
+// Combines the nw run records of one (group, head) per workgroup. Thread t
+// owns output dims 4 (t % (D/4)) .. +3 and the records s = t / (D/4) + k*RS:
+// it keeps a running (m, l, acc) over its few records (all loads independent,
+// so one memory round trip), then the RS partials of each dim combine through
+// LDS with the same stable rescaling.
 template <int D, int G>
 __global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p) {
-  constexpr int HDR = (2 * G + 3) & ~3;
+  constexpr int HDR = record_header(G);
   constexpr int REC = HDR + G * D;
-  extern __shared__ float lds[];  // w[G][splits], inv_l[G]
-  const int grp = blockIdx.x;
+  constexpr int C4 = D / 4;          // threads per record (one float4 of dims each)
+  constexpr int RS = 256 / C4;       // record subsets
+  __shared__ float sm[RS], sl[RS];
+  __shared__ float4 sa[RS][C4];
   const int per_item = p.n_head_kv * p.n_chunks;
+  const int grp = blockIdx.x / G;
+  const int h = blockIdx.x % G;
   const DecodeItem& it = p.item[grp / per_item];
-  const int g = (grp % per_item) / p.n_chunks;
-  const int hc = grp % p.n_chunks;
-  const int head0 = g * p.n_rep + hc * G;
-  const int S = p.splits;
-  const float* base = p.part + (int64_t)grp * S * REC;
-  float* w = lds;
-  float* inv_l = lds + G * S;
+  const int S = it.nw;
+  if (S == 1) return;  // written by its only run
+  const int gl = grp % per_item;
+  const int g = gl / p.n_chunks;
+  const int hc = gl % p.n_chunks;
+  const int head = g * p.n_rep + hc * G + h;
+  const float* base = p.part + (int64_t)(it.wave0 + gl * S) * REC;
+  const int c4 = threadIdx.x % C4, sub = threadIdx.x / C4;
 
-  // pass 1: one wave per head (round robin), lanes over splits
-  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-  for (int h = wv; h < G; h += blockDim.x / kWave) {
-    float mx = -INFINITY;
-    for (int sp = lane; sp < S; sp += kWave) mx = fmaxf(mx, base[(int64_t)sp * REC + h]);
-    mx = wave_max_dpp(mx);
-    float den = 0.f;
-    for (int sp = lane; sp < S; sp += kWave) {
-      const float* r = base + (int64_t)sp * REC;
-      const float wt = fast_exp2(r[h] - mx);  // empty split: m = -inf -> 0
-      w[h * S + sp] = wt;
-      den += wt * r[G + h];
-    }
-    den = wave_sum(den);
-    if (lane == 0) inv_l[h] = 1.f / den;
+  float m = -INFINITY, l = 0.f;
+  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+  for (int s = sub; s < S; s += RS) {
+    const float* r = base + (int64_t)s * REC;
+    const float ms = r[h], ls = r[G + h];
+    const float4 as = *reinterpret_cast<const float4*>(r + HDR + h * D + 4 * c4);
+    const float mn = fmaxf(m, ms);
+    const float wo = fast_exp2(m - mn), wn = fast_exp2(ms - mn);
+    l = l * wo + ls * wn;
+    a.x = a.x * wo + as.x * wn;
+    a.y = a.y * wo + as.y * wn;
+    a.z = a.z * wo + as.z * wn;
+    a.w = a.w * wo + as.w * wn;
+    m = mn;
   }
+  if (c4 == 0) {
+    sm[sub] = m;
+    sl[sub] = l;
+  }
+  sa[sub][c4] = a;
   __syncthreads();
-
-  // pass 2: independent weighted sums
-  for (int idx = threadIdx.x; idx < G * D; idx += blockDim.x) {
-    const int h = idx / D, d = idx % D;
-    const float* a = base + HDR + h * D + d;
-    const float* wh = w + h * S;
-    // 8 independent loads per round keep the split records' latency overlapped.
-    float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int sp = 0;
-    for (; sp + 8 <= S; sp += 8) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) acc8[u] = fmaf(wh[sp + u], a[(int64_t)(sp + u) * REC], acc8[u]);
-    }
-    for (; sp < S; ++sp) acc8[0] = fmaf(wh[sp], a[(int64_t)sp * REC], acc8[0]);
-    float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) +
-                                        (int64_t)(head0 + h) * it.o_s1);
-    o[d] = (((acc8[0] + acc8[1]) + (acc8[2] + acc8[3])) + ((acc8[4] + acc8[5]) + (acc8[6] + acc8[7]))) *
-           inv_l[h];
+  if (sub != 0) return;
+  float mx = -INFINITY;
+  for (int k = 0; k < RS; ++k) mx = fmaxf(mx, sm[k]);
+  float lt = 0.f;
+  float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k = 0; k < RS; ++k) {
+    const float wk = sm[k] == -INFINITY ? 0.f : fast_exp2(sm[k] - mx);  // subset with no record
+    lt += wk * sl[k];
+    const float4 ak = sa[k][c4];
+    at.x += wk * ak.x;
+    at.y += wk * ak.y;
+    at.z += wk * ak.z;
+    at.w += wk * ak.w;
   }
+  const float inv = 1.f / lt;
+  float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) + (int64_t)head * it.o_s1);
+  *reinterpret_cast<float4*>(o + 4 * c4) = make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
+}
+
+// Depth 1 (two waves per SIMD) for head_dim 64; head_dim 128 tiles do not fit
+// 256 registers with a refill in flight, so they run at depth 2 (one wave per
+// SIMD). MI_HIP_DECODE_DEPTH=1|2 overrides (tuning).
+int decode_depth(int head_dim) {
+  static const int forced = [] {
+    const char* e = std::getenv("MI_HIP_DECODE_DEPTH");
+    return e && (e[0] == '1' || e[0] == '2') ? e[0] - '0' : 0;
+  }();
+  return forced ? forced : (head_dim == 64 ? 1 : 2);
 }
 
 template <int D, typename KT, int G>
-static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
-  const size_t lds_max = (size_t)kDecodeWaves * kDecodeTile * 64 * sizeof(float);
-  // head_dim 64: two waves per SIMD unless MI_HIP_DECODE_WIDE=1; head_dim 128: one.
-  static const bool wide = D > 64 || [] {
-    const char* e = std::getenv("MI_HIP_DECODE_WIDE");
-    return e && e[0] == '1';
-  }();
-  const void* fn = wide ? reinterpret_cast<const void*>(&decode_kernel_wide<D, KT, G>)
-                        : reinterpret_cast<const void*>(&decode_kernel<D, KT, G>);
-  static const hipError_t attr = hipFuncSetAttribute(
-      fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
-  if (attr != hipSuccess) return attr;
-  const unsigned groups = (unsigned)(p.n_items * p.n_head_kv * p.n_chunks);
-  const size_t lds = (size_t)p.waves * kDecodeTile * 64 * sizeof(float);
-  if (wide)
-    hipLaunchKernelGGL((decode_kernel_wide<D, KT, G>), dim3((unsigned)p.splits, groups),
-                       dim3(p.waves * kWave), lds, stream, p);
+static hipError_t launch_decode_t(const DecodeParams& p, int max_nw, hipStream_t stream) {
+  if (decode_depth(D) == 2)
+    hipLaunchKernelGGL((decode_kernel_deep<D, KT, G>), dim3((unsigned)p.n_waves), dim3(kWave), 0,
+                       stream, p);
   else
-    hipLaunchKernelGGL((decode_kernel<D, KT, G>), dim3((unsigned)p.splits, groups),
-                       dim3(p.waves * kWave), lds, stream, p);
+    hipLaunchKernelGGL((decode_kernel<D, KT, G>), dim3((unsigned)p.n_waves), dim3(kWave), 0,
+                       stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.splits == 1) return e;
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(groups), dim3(256),
-                     ((size_t)G * p.splits + G) * sizeof(float), stream, p);
+  if (e != hipSuccess || max_nw <= 1) return e;
+  const unsigned groups = (unsigned)(p.n_items * p.n_head_kv * p.n_chunks);
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(groups * G), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
 template <int D, typename KT>
-static hipError_t launch_decode_g(const DecodeParams& p, int g, hipStream_t stream) {
+static hipError_t launch_decode_g(const DecodeParams& p, int g, int max_nw, hipStream_t stream) {
   switch (g) {
-    case 1: return launch_decode_t<D, KT, 1>(p, stream);
-    case 2: return launch_decode_t<D, KT, 2>(p, stream);
-    case 4: return launch_decode_t<D, KT, 4>(p, stream);
-    case 7: return launch_decode_t<D, KT, 7>(p, stream);
-    case 8: return launch_decode_t<D, KT, 8>(p, stream);
+    case 1: return launch_decode_t<D, KT, 1>(p, max_nw, stream);
+    case 2: return launch_decode_t<D, KT, 2>(p, max_nw, stream);
+    case 4: return launch_decode_t<D, KT, 4>(p, max_nw, stream);
+    case 7: return launch_decode_t<D, KT, 7>(p, max_nw, stream);
+    case 8: return launch_decode_t<D, KT, 8>(p, max_nw, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -400,18 +469,17 @@ int decode_group_size(int n_rep) {
 }
 
 size_t decode_record_floats(int head_dim, int group) {
-  const int hdr = (2 * group + 3) & ~3;
-  return (size_t)hdr + (size_t)group * head_dim;
+  return (size_t)record_header(group) + (size_t)group * head_dim;
 }
 
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, int max_nw,
                          hipStream_t stream) {
   if (head_dim == 64)
-    return f16 ? launch_decode_g<64, _Float16>(p, group, stream)
-               : launch_decode_g<64, float>(p, group, stream);
+    return f16 ? launch_decode_g<64, _Float16>(p, group, max_nw, stream)
+               : launch_decode_g<64, float>(p, group, max_nw, stream);
   if (head_dim == 128)
-    return f16 ? launch_decode_g<128, _Float16>(p, group, stream)
-               : launch_decode_g<128, float>(p, group, stream);
+    return f16 ? launch_decode_g<128, _Float16>(p, group, max_nw, stream)
+               : launch_decode_g<128, float>(p, group, max_nw, stream);
   return hipErrorInvalidValue;
 }
 

@@ -12,8 +12,10 @@ namespace mi {
 
 // decode.hip
 int decode_group_size(int n_rep);                       // G: Q heads per wave group
+int decode_depth(int head_dim);                         // K/V tiles in flight per wave (1, 2)
 size_t decode_record_floats(int head_dim, int group);   // floats per split partial
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
+// max_nw: the largest runs-per-group of any item (1: no merge launch).
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, int max_nw,
                          hipStream_t stream);
 
 // prefill.hip

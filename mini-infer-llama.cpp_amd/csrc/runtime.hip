@@ -11,6 +11,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -61,6 +62,7 @@ struct State {
   // of split prefill query blocks), grown on demand, never shrunk.
   char* ws = nullptr;
   size_t ws_bytes = 0;
+  int n_cu = 0;  // compute units of the device
 };
 State g;
 
@@ -125,32 +127,52 @@ int env_int(const char* name, int dflt) {
 // ---------------------------------------------------------------------------
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Waves a decode launch aims for: as many as the SIMDs hold at once (two per
+// SIMD at depth 1, one at depth 2).
+int decode_wave_target(int head_dim) {
+  const int forced = env_int("MI_HIP_DECODE_WAVES", 0);
+  return forced > 0 ? forced : std::max(1, 4 * g.n_cu * (mi::decode_depth(head_dim) == 2 ? 1 : 2));
+}
+
 struct DecodePlan {
-  int group = 1, n_chunks = 1, splits = 1, waves = 1;
+  int group = 1, n_chunks = 1;
+  int n_waves = 0, max_nw = 1;
   size_t part_floats = 0;
 };
 
-// Splits per (item, head chunk) so the launch has about `target` workgroups,
-// each split at least one 64-position tile; one wave per tile of a split up
-// to kDecodeWaves.
-DecodePlan plan_decode(int n_items, int n_head_kv, int n_rep, int head_dim, int max_n_kv) {
+// Runs per group for each item: about `decode_wave_target()` waves in total,
+// shared out in proportion to the items' tile counts, each run at least one
+// 64-position tile. Fills wave0/nw of the items.
+DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim) {
   DecodePlan p;
   p.group = mi::decode_group_size(n_rep);
   p.n_chunks = n_rep / p.group;
-  const int groups = n_items * n_head_kv * p.n_chunks;
-  const int target = std::max(1, env_int("MI_HIP_DECODE_WGS", 256));
-  // at least one tile per wave of a full workgroup when the grid is small
-  const int max_splits =
-      std::max(1, (max_n_kv + mi::kDecodeTile * mi::kDecodeWaves - 1) / (mi::kDecodeTile * mi::kDecodeWaves));
-  int s = (target + groups - 1) / groups;
-  const int forced = env_int("MI_HIP_DECODE_SPLITS", 0);
-  if (forced > 0) s = forced;
-  p.splits = std::max(1, std::min(s, max_splits));
-  // one wave per 64-position tile of a split, up to kDecodeWaves
-  const int per_split = ((max_n_kv + p.splits - 1) / p.splits + mi::kDecodeTile - 1) / mi::kDecodeTile;
-  p.waves = std::max(1, std::min(mi::kDecodeWaves, per_split));
-  p.part_floats = p.splits > 1 ? (size_t)groups * p.splits * mi::decode_record_floats(head_dim, p.group) : 0;
+  const int per_item = n_head_kv * p.n_chunks;
+  int64_t tiles = 0;
+  for (int i = 0; i < n_items; ++i)
+    tiles += (int64_t)per_item * ((it[i].n_kv + mi::kDecodeTile - 1) / mi::kDecodeTile);
+  const int64_t target = decode_wave_target(head_dim);
+  int64_t waves = 0;
+  for (int i = 0; i < n_items; ++i) {
+    const int64_t tpg = (it[i].n_kv + mi::kDecodeTile - 1) / mi::kDecodeTile;
+    const int nw = (int)std::max<int64_t>(1, std::min<int64_t>(tpg, tpg * target / tiles));
+    it[i].wave0 = (int32_t)waves;
+    it[i].nw = nw;
+    waves += (int64_t)per_item * nw;
+    p.max_nw = std::max(p.max_nw, nw);
+  }
+  p.n_waves = (int)waves;
+  p.part_floats = p.max_nw > 1 ? (size_t)waves * mi::decode_record_floats(head_dim, p.group) : 0;
   return p;
+}
+
+// Records for any decode launch of up to kDecodeMaxItems items of this shape:
+// the proportional shares sum to at most the target, plus one per group for
+// the at-least-one rounding.
+size_t decode_part_bound(int n_head_kv, int n_rep, int head_dim) {
+  const int group = mi::decode_group_size(n_rep);
+  const int64_t groups = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group);
+  return (size_t)(decode_wave_target(head_dim) + groups) * mi::decode_record_floats(head_dim, group);
 }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -276,13 +298,7 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
   Resolved r0;
   int rc = resolve_kv(&items[0], &r0);
   if (rc) return rc;
-  int max_n_kv = 0;
-  for (int i = 0; i < n; ++i) max_n_kv = std::max(max_n_kv, items[i].n_past + 1);
-  const int chunk_items = std::min(n, mi::kDecodeMaxItems);
-  const DecodePlan plan =
-      plan_decode(chunk_items, r0.n_head_kv, items[0].n_rep, r0.head_dim, max_n_kv);
-  rc = ensure_workspace(plan.part_floats * sizeof(float));
-  if (rc) return rc;
+  const int elt = r0.f16 ? 2 : 4;
   for (int base = 0; base < n; base += mi::kDecodeMaxItems) {
     const int cnt = std::min(mi::kDecodeMaxItems, n - base);
     mi::DecodeParams p{};
@@ -291,16 +307,23 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
       rc = resolve_kv(&items[base + i], &r);
       if (rc) return rc;
       p.item[i] = make_item(&items[base + i], r);
+      // the kernel addresses one KV head's rows with 32-bit byte offsets
+      const int64_t last = (int64_t)(p.item[i].n_kv - 1);
+      if (last * r.k_s2 + (int64_t)r.head_dim * elt > INT32_MAX ||
+          last * r.v_s2 + (int64_t)r.head_dim * elt > INT32_MAX)
+        return fail(MI_HIP_E_UNSUPPORTED,
+                    "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + i);
     }
+    const DecodePlan plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim);
+    if ((rc = ensure_workspace(plan.part_floats * sizeof(float)))) return rc;
     p.n_items = cnt;
     p.n_rep = items[0].n_rep;
     p.n_head_kv = r0.n_head_kv;
     p.n_chunks = plan.n_chunks;
-    p.splits = plan.splits;
-    p.waves = plan.waves;
+    p.n_waves = plan.n_waves;
     p.scale_log2e = items[0].scale * kLog2e;
     p.part = ws_part();
-    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, stream);
+    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, plan.max_nw, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
   }
   return MI_HIP_OK;
@@ -331,11 +354,9 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   return MI_HIP_OK;
 }
 
-// Workspace bytes that cover every decode call up to n_ctx (prefill needs none).
+// Workspace bytes that cover every decode call on this cache (prefill needs none).
 size_t workspace_for(const mi_hip_kv_desc& d) {
-  const int n_rep = d.n_head / d.n_head_kv;
-  const DecodePlan dp = plan_decode(1, d.n_head_kv, n_rep, d.head_dim, d.n_ctx);
-  return dp.part_floats * sizeof(float);
+  return decode_part_bound(d.n_head_kv, d.n_head / d.n_head_kv, d.head_dim) * sizeof(float);
 }
 
 // ---------------------------------------------------------------------------
@@ -510,6 +531,7 @@ int mi_hip_init(int device) {
                 prop.gcnArchName);
   MI_TRY_HIP(hipSetDevice(device), "hipSetDevice");
   g.device = device;
+  g.n_cu = prop.multiProcessorCount;
   g.ready = true;
   t_err[0] = '\0';
   return MI_HIP_OK;
