@@ -96,8 +96,10 @@ typedef struct mi_hip_kv_desc {
 
 /* One device allocation holding every layer's K and V as
  * [head_dim, n_head_kv, n_ctx] (position-major, the layout of
- * src/model_qwen2.cpp:564-577), plus the split-KV workspace and the host-node
- * staging buffers, all sized for n_ctx. Nothing is allocated afterwards.
+ * src/model_qwen2.cpp:564-577), plus the host-node staging buffer (sized for
+ * n_ctx) and the library's split-KV workspace (grown, if needed, to cover a
+ * decode launch of up to 32 items of this head shape). Nothing is allocated
+ * afterwards.
  * Replaces mi_kv_cache_init's host KV context (src/model_qwen2.cpp:564-577). */
 int mi_hip_kv_create(const mi_hip_kv_desc* desc, mi_hip_kv** out);
 int mi_hip_kv_destroy(mi_hip_kv* kv);

@@ -141,6 +141,18 @@ def test_brute_force_check_catches_planted_mistakes(oracle):
     assert not np.allclose(wrong_gqa, s64, rtol=1e-5, atol=1e-5)
     shifted = np.roll(p, 1, axis=2)  # mask one key too late
     assert not np.allclose(shifted, p64, rtol=1e-5, atol=1e-6)
+    # A dropped term (the last head dimension left out of the dot product).
+    dropped = s.copy()
+    for hh in range(h):
+        dropped[hh] = (k[: n_past + t, hh // (h // hkv), : d - 1] @ q[:, hh, : d - 1].T).T
+    assert not np.allclose(dropped, s64, rtol=1e-5, atol=1e-5)
+    # P.V with the probabilities of the wrong query row (an index slip in j).
+    wrong_row = o.copy()
+    for hh in range(h):
+        pv = p64[hh, np.r_[1:t, 0], :]  # row j uses query j+1's probabilities
+        wrong_row[:, hh, :] = pv @ v[: n_past + t, hh // (h // hkv), :].astype(np.float64)
+    assert not np.allclose(wrong_row, o64, rtol=1e-5, atol=1e-5)
+    assert np.allclose(o, o64, rtol=1e-5, atol=1e-5)
 
 
 def test_invariants(oracle):
@@ -172,6 +184,13 @@ def test_invariants(oracle):
     assert np.all(p == 1.0)
     for hh in range(h):
         assert np.array_equal(o[0, hh], v[0, hh // n_rep])
+    # Identical keys give uniform probabilities 1/N and the mean of the V rows.
+    k_same = np.broadcast_to(k[:1], k.shape).copy()
+    s, p, o = oracle.attention(q[:1], k_same, v, 47, scale, 1)
+    assert np.all(p == p[0, 0, 0]) and abs(p[0, 0, 0] - 1.0 / 48) < 1e-9
+    for hh in range(h):
+        assert np.allclose(o[0, hh], v[:48, hh // n_rep].astype(np.float64).mean(axis=0),
+                           rtol=1e-5, atol=1e-6)
     # Permuting cached positions permutes the scores (decode).
     perm = np.random.default_rng(1).permutation(48)
     s0, _, o0 = oracle.attention(q[:1], k, v, 47, scale, 1)
