@@ -13,7 +13,8 @@ constexpr int kWave = 64;
 // Decode (one query token against n_kv cached positions).
 // ---------------------------------------------------------------------------
 constexpr int kDecodeMaxItems = 32;  // items per launch (they ride in kernarg)
-constexpr int kDecodeTile = 64;      // positions per tile (lane = position in QK)
+constexpr int kDecodeSub = 16;       // positions per sub-tile (one wave's unit of work)
+constexpr int kDecodeWaves = 4;      // waves per workgroup (one per SIMD)
 
 // One independent decode problem. Byte strides; the head_dim axis of K, V, Q
 // and O is contiguous.
@@ -27,24 +28,26 @@ struct DecodeItem {
   int64_t q_s1;        // Q: bytes between heads
   int64_t o_s1;        // O: bytes between heads
   int32_t n_kv;        // keys [0, n_kv) are visible
-  int32_t wave0;       // first wave (= workgroup) of this item
-  int32_t nw;          // waves per (KV head, head chunk) group
-  int32_t pad_;
+  int32_t spg;         // sub-tiles per group: ceil(n_kv / kDecodeSub)
+  int32_t wg0;         // first workgroup of this item
+  int32_t kpg;         // workgroups per group
 };
 
-// Work decomposition: a "group" is (item, KV head g, head chunk hc), i.e. the
-// G Q heads g*n_rep + hc*G .. + G - 1 that read KV head g. Its ceil(n_kv/64)
-// position tiles are split into nw contiguous runs, one per wave; each wave is
-// one workgroup. Waves of an item are numbered group-major from wave0.
+// Work decomposition. A group is (item, KV head g, head chunk hc): the G Q
+// heads g*n_rep + hc*G .. + G - 1 that read KV head g. Each group is served by
+// kpg workgroups of its item; workgroup wg0 + gl*kpg + part owns sub-tiles
+// [spg*part/kpg, spg*(part+1)/kpg) of the item's group gl and leaves one
+// record when kpg > 1.
 struct DecodeParams {
   DecodeItem item[kDecodeMaxItems];
   int32_t n_items;
   int32_t n_rep;        // Q heads per KV head
   int32_t n_head_kv;
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
-  int32_t n_waves;      // total waves (grid size)
+  int32_t n_wg;         // workgroups
   float scale_log2e;    // softmax scale * log2(e)
-  float* part;          // one (m, l, acc) record per wave when nw > 1
+  float* rec;           // one record per workgroup
+  unsigned* cnt;        // one arrival counter per (item, group); zero between launches
 };
 
 // ---------------------------------------------------------------------------

@@ -1,485 +1,689 @@
 // decode.hip -- fused ATTN_QK -> causal SOFTMAX -> ATTN_KQV for one query
 // token (src/ops_cpu.cpp:304-410 with n_tokens == 1), HBM-bound, no MFMA.
 //
-// Work decomposition. A group is (item, KV head g, head chunk hc): the G Q
-// heads g*n_rep + hc*G .. + G - 1 that read KV head g (GQA is an index
-// mapping: every K/V row is read once for all G heads, never copied). A
-// group's positions form ceil(n_kv / 64) tiles, split into nw contiguous runs,
-// one per wave; each wave is a workgroup of its own. The host sizes nw so the
-// launch has about one wave per SIMD and every run has the same number of
-// tiles to within one.
+// One launch, one kernel, no second pass.
 //
-// Per wave: the G query vectors stay in registers, spread over the 16 lanes of
-// each row. The K and V tiles of NBUF tiles are requested up front and each
-// slot is refilled as soon as its registers are free, so every wave keeps one
-// to two tiles of HBM requests in flight while it computes. Loads go through
-// buffer resources bounded by the group's last row: rows past n_kv read as
-// zero without a memory request, and so do refills past the run's end (a
-// zero-sized resource), which keeps the loop free of branches around loads.
-// Per tile:
-//   1. K rows go to a swizzled LDS tile and lane i takes position i: each
-//      lane dots its row with the G queries, whose elements reach every lane
-//      as DPP row-broadcast FMA operands (no memory round trip);
-//   2. online softmax in base 2: running max by DPP row reduction + readlane,
-//      exp2 of log2e-prescaled scores; probabilities to LDS;
-//   3. P.V with lanes owning 4 output dims of one row, V straight from the
-//      registers it was loaded into.
-// A run that covers its whole group writes O; otherwise the wave writes an
-// (m, l, acc) record and decode_merge_kernel, launched next on the same
-// stream, combines the nw records of each group with the stable rescaling
-// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s.
-// (No cross-workgroup signalling inside a kernel: on this part a device-scope
-// fence writes back and invalidates the whole L2 of the XCD.)
+// Work decomposition. A group is (item, KV head g, head chunk hc): the G <= 4*HS
+// Q heads that read KV head g (GQA is an index mapping: every K/V row is read
+// once for all G heads, never copied). Each group is served by kpg workgroups
+// (the host sizes kpg so the launch has about one workgroup per CU); workgroup
+// part p owns a contiguous share of the group's 16-position sub-tiles, and its
+// NWV waves take the share's sub-tiles round-robin. A workgroup never changes
+// group, so its waves never meet before the end.
+//
+// Streaming. Each wave owns an LDS ring of NB slots; a slot holds one
+// sub-tile's K rows then its V rows, written by buffer_load ... lds (direct to
+// LDS, no registers). Every refill is issued -- past the wave's last sub-tile
+// through a zero-sized resource that reads nothing -- so the number of loads
+// issued after any slot's K (or V) is always the same and the waits are fixed
+// vmcnt values. Rows past n_kv lie outside the group's bounded resource and
+// arrive as zeros. The 16-byte slots of each K row are stored XOR-swizzled by
+// row, so the lane-per-row reads below are free of bank conflicts.
+//
+// Per sub-tile (lane = (row r = lane / 16, column i = lane % 16)):
+//   QK  lane (position i, head slots r + 4h): the lane dots its K row with the
+//       query, whose elements come from a DPP row broadcast (v_fmac_f32_dpp
+//       row_newbcast) -- the queries stay spread over the 16 lanes of a row;
+//   softmax in base 2, running max per head by DPP row reduction;
+//   PV  lane (dims 4i + 64e .., head slots r + 4h): O += P.V with plain FMAs;
+//       the 16 probabilities of a row go through a small per-wave LDS area and
+//       come back as a broadcast read.
+//
+// Combining. At the end the waves' (m, l, acc) meet in LDS. With kpg == 1 the
+// workgroup writes O. Otherwise it writes one record (agent-scope atomic
+// stores, which bypass the non-coherent L2) and bumps the group's arrival
+// counter; the workgroup that arrives last reads the group's kpg records
+// (agent-scope atomic loads) and writes O with the stable rescaling
+// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s, then re-arms the counter.
+// Ordering without fences: each wave waits for its record stores (vmcnt 0)
+// before the workgroup barrier that precedes the counter increment, and the
+// reader issues its loads only after the increment returned. (A device-scope
+// fence would write back and invalidate the XCD's whole L2 instead.)
 #include <cstdlib>
+#include <type_traits>
 
 #include "attn_common.h"
 #include "kernels.h"
 
 namespace mi {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+// Cache policy of buffer accesses that must be coherent across the XCDs' L2
+// caches (the encoding the compiler uses for agent-scope atomic loads/stores).
+constexpr int kSc1 = 16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
 // Raw (unswizzled, stride 0) buffer descriptor word 3 of the gfx9 family.
 constexpr int kRawBufferWord3 = 0x00020000;
 
-// Descriptor over [p, p + bytes): loads at offsets >= bytes return zero and
-// make no memory request.
-__device__ inline rsrc_t make_rsrc(const char* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(p), (short)0, (int)bytes,
+// Descriptor over [p, p + bytes): 16-byte accesses at offsets >= bytes read
+// zero and make no memory request.
+__device__ inline rsrc_t make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
                                            kRawBufferWord3);
 }
 
-// Four consecutive cache elements, held in registers at storage width.
-template <typename KT>
-struct Cache;
-template <>
-struct Cache<float> {
-  typedef f32x4 raw;
-  static __device__ inline raw load(rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-  }
-  static __device__ inline float4 widen(raw x) { return make_float4(x.x, x.y, x.z, x.w); }
-};
-template <>
-struct Cache<_Float16> {
-  typedef half4_t raw;
-  static __device__ inline raw load(rsrc_t r, unsigned off) {
-    return __builtin_bit_cast(half4_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
-  }
-  static __device__ inline float4 widen(raw h) {
-    return make_float4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
-  }
-};
+template <int N>
+__device__ inline void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ inline void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Record of one wave's run: m[G], l[G] (padded to 4), then acc[G][D].
-__host__ __device__ constexpr int record_header(int g) { return (2 * g + 3) & ~3; }
-
-// s[J % NACC][h] += bcast_J(q[h]) * k for all heads; heads are interleaved so
-// the DPP operand of an instruction was written at least two instructions
-// earlier (no hazard wait states).
-template <int J, int G, int NACC>
-__device__ __forceinline__ void qk_step(float (&s)[NACC][G], const float (&q)[G], float k) {
-#pragma unroll
-  for (int h = 0; h < G; ++h) s[J % NACC][h] = fmac_bcast<J>(s[J % NACC][h], q[h], k);
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
-// DEPTH: tiles of K/V requested ahead per wave. Depth 1 keeps the wave within
-// 256 registers, so each SIMD runs two waves and one computes while the other
-// waits on memory; depth 2 holds two tiles (one wave per SIMD).
-template <int D, typename KT, int G, int DEPTH>
-__device__ __forceinline__ void decode_body(const DecodeParams& p) {
-  typedef Cache<KT> C;
-  typedef typename C::raw raw_t;
-  constexpr int ELT = (int)sizeof(KT);
-  constexpr int NCH = D / 64;                 // 64-dim K chunks per row
-  constexpr int NK = NCH * 16;                // K loads per lane per tile
-  constexpr int LPR = D / 4;                  // PV: lanes per V row
-  constexpr int RPI = kWave / LPR;            // PV: rows per load
-  constexpr int NV = kDecodeTile / RPI;       // V loads per lane per tile
-  constexpr int NBUF = DEPTH;
-  constexpr int NACC = G >= 3 ? 1 : (G == 2 ? 2 : 3);
-  constexpr int HDR = record_header(G);
-  constexpr int REC = HDR + G * D;
-  constexpr int CS = kDecodeTile * 64;        // LDS floats per staged K chunk
+// Physical 16-byte slot of logical slot j in row r is j ^ swz(r).
+template <int NSLOT>
+__host__ __device__ constexpr int swz(int r) {
+  return NSLOT >= 16 ? (r & 15) : ((r >> 1) & (NSLOT - 1));
+}
 
-  __shared__ float klds[NCH * CS];  // the K tile (F32, swizzled), then P
+__device__ inline float row_sum16(float x) {
+  x += dpp_mov<0xB1>(x);
+  x += dpp_mov<0x4E>(x);
+  x += dpp_mov<0x141>(x);
+  x += dpp_mov<0x140>(x);
+  return x;
+}
 
-  const int lane = threadIdx.x;
-  const int wid = blockIdx.x;
+typedef __attribute__((address_space(3))) char lds_t;
+typedef __attribute__((address_space(3))) const DecodeItem lds_item_t;
 
-  // item, group and run of this wave (items are few: a scalar scan)
-  int ii = 0;
-  while (ii + 1 < p.n_items && wid >= p.item[ii + 1].wave0) ++ii;
-  const DecodeItem& it = p.item[ii];
-  const int local = wid - it.wave0;
-  const int gl = local / it.nw;
-  const int run = local - gl * it.nw;
-  const int g = gl / p.n_chunks;
-  const int hc = gl - g * p.n_chunks;
-  const int head0 = g * p.n_rep + hc * G;
-  const int n_kv = it.n_kv;
-  const int tpg = (n_kv + kDecodeTile - 1) / kDecodeTile;
-  const int t_begin = (int)((int64_t)tpg * run / it.nw);
-  const int t_end = (int)((int64_t)tpg * (run + 1) / it.nw);
+// Wave-uniform copies of values read from LDS (the compiler cannot prove a
+// load from a uniform LDS address uniform; buffer resources must be scalar).
+__device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ inline int64_t uni(int64_t x) {
+  const uint64_t u = (uint64_t)x;
+  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
+                   (uint32_t)__builtin_amdgcn_readfirstlane((int)u));
+}
+template <typename T>
+__device__ inline T* uni(T* x) {
+  return reinterpret_cast<T*>(uni((int64_t)reinterpret_cast<uintptr_t>(x)));
+}
 
-  // Offsets are 32-bit (the host checks n_kv * stride < 2^31).
-  const int ks2 = (int)it.k_s2, vs2 = (int)it.v_s2;
-  const rsrc_t kres = make_rsrc(it.k + (int64_t)g * it.k_s1, (unsigned)((n_kv - 1) * ks2 + D * ELT));
-  const rsrc_t vres = make_rsrc(it.v + (int64_t)g * it.v_s1, (unsigned)((n_kv - 1) * vs2 + D * ELT));
-  const rsrc_t none = make_rsrc(it.k, 0u);
+// The launch's item table, staged in LDS at kernel start: kernel arguments are
+// read once, in one parallel round trip, instead of by dependent scalar loads.
+__device__ inline lds_item_t& item_at(const lds_t* tab, int i) {
+  return reinterpret_cast<lds_item_t*>(tab)[i];
+}
 
-  const int kr = lane >> 4, kc = lane & 15;    // K staging: 16 lanes per 64-dim chunk row
-  const int vr = lane / LPR, vc = lane % LPR;  // PV: LPR lanes per V row
-  const unsigned klane = (unsigned)(kr * ks2 + kc * 4 * ELT);
-  const unsigned vlane = (unsigned)(vr * vs2 + vc * 4 * ELT);
+// ---------------------------------------------------------------------------
+// DPP multiply-add blocks. v_fmac_f32_dpp with row_newbcast:J takes its first
+// factor from lane J of each row of 16. The compiler does not form it (the
+// accumulator is tied), so each block is one asm statement with a fixed
+// order: no accumulator is written by two DPP instructions less than three
+// instructions apart, and the first block of a chain initialises its
+// accumulators with v_mul_f32_dpp inside the block. Inputs written by a VALU
+// instruction (probabilities, rescaled accumulators, widened F16 elements) are
+// separated from the block by an s_nop 1 (two wait states): NOP prefixes the
+// block with it.
+// ---------------------------------------------------------------------------
+#define MI_DPP(op, d, q, k, j) #op "_dpp %" #d ", %" #q ", %" #k " row_newbcast:%" #j " row_mask:0xf bank_mask:0xf\n\t"
+#define MI_NOP "s_nop 1\n\t"
 
-  // The G query vectors, requested before any cache tile:
-  // qv[h][c] = Q[head0 + h][16 c + (lane & 15)].
-  float qv[G][D / 16];
+// QK, four elements of one source lane J: s[h][e % (4/HS)] += bcast_J(q[h][e]) * k[e].
+#define MI_QK2_FIRST                                                              \
+  MI_DPP(v_mul_f32, 0, 4, 12, 16) MI_DPP(v_mul_f32, 2, 8, 12, 16)                 \
+  MI_DPP(v_mul_f32, 1, 5, 13, 16) MI_DPP(v_mul_f32, 3, 9, 13, 16)                 \
+  MI_DPP(v_fmac_f32, 0, 6, 14, 16) MI_DPP(v_fmac_f32, 2, 10, 14, 16)              \
+  MI_DPP(v_fmac_f32, 1, 7, 15, 16) MI_DPP(v_fmac_f32, 3, 11, 15, 16)
+#define MI_QK2_NEXT                                                               \
+  MI_DPP(v_fmac_f32, 0, 4, 12, 16) MI_DPP(v_fmac_f32, 2, 8, 12, 16)               \
+  MI_DPP(v_fmac_f32, 1, 5, 13, 16) MI_DPP(v_fmac_f32, 3, 9, 13, 16)               \
+  MI_DPP(v_fmac_f32, 0, 6, 14, 16) MI_DPP(v_fmac_f32, 2, 10, 14, 16)              \
+  MI_DPP(v_fmac_f32, 1, 7, 15, 16) MI_DPP(v_fmac_f32, 3, 11, 15, 16)
+#define MI_QK2_IN                                                                 \
+  "v"(q[0][0]), "v"(q[0][1]), "v"(q[0][2]), "v"(q[0][3]), "v"(q[1][0]), "v"(q[1][1]), \
+      "v"(q[1][2]), "v"(q[1][3]), "v"(k[0]), "v"(k[1]), "v"(k[2]), "v"(k[3]), "i"(J)
+#define MI_QK1_FIRST                                                              \
+  MI_DPP(v_mul_f32, 0, 4, 8, 12) MI_DPP(v_mul_f32, 1, 5, 9, 12)                   \
+  MI_DPP(v_mul_f32, 2, 6, 10, 12) MI_DPP(v_mul_f32, 3, 7, 11, 12)
+#define MI_QK1_NEXT                                                               \
+  MI_DPP(v_fmac_f32, 0, 4, 8, 12) MI_DPP(v_fmac_f32, 1, 5, 9, 12)                 \
+  MI_DPP(v_fmac_f32, 2, 6, 10, 12) MI_DPP(v_fmac_f32, 3, 7, 11, 12)
+#define MI_QK1_IN                                                                 \
+  "v"(q[0][0]), "v"(q[0][1]), "v"(q[0][2]), "v"(q[0][3]), "v"(k[0]), "v"(k[1]), "v"(k[2]), \
+      "v"(k[3]), "i"(J)
+
+template <int J, bool FIRST, bool NOP>
+__device__ __forceinline__ void qk4_2(float (&s)[2][2], const float (&q)[2][4], const float (&k)[4]) {
+#define MI_OUT_W "=&v"(s[0][0]), "=&v"(s[0][1]), "=&v"(s[1][0]), "=&v"(s[1][1])
+#define MI_OUT_RW "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[1][0]), "+v"(s[1][1])
+  if constexpr (FIRST && NOP) asm(MI_NOP MI_QK2_FIRST : MI_OUT_W : MI_QK2_IN);
+  else if constexpr (FIRST) asm(MI_QK2_FIRST : MI_OUT_W : MI_QK2_IN);
+  else if constexpr (NOP) asm(MI_NOP MI_QK2_NEXT : MI_OUT_RW : MI_QK2_IN);
+  else asm(MI_QK2_NEXT : MI_OUT_RW : MI_QK2_IN);
+#undef MI_OUT_W
+#undef MI_OUT_RW
+}
+
+template <int J, bool FIRST, bool NOP>
+__device__ __forceinline__ void qk4_1(float (&s)[1][4], const float (&q)[1][4], const float (&k)[4]) {
+#define MI_OUT_W "=&v"(s[0][0]), "=&v"(s[0][1]), "=&v"(s[0][2]), "=&v"(s[0][3])
+#define MI_OUT_RW "+v"(s[0][0]), "+v"(s[0][1]), "+v"(s[0][2]), "+v"(s[0][3])
+  if constexpr (FIRST && NOP) asm(MI_NOP MI_QK1_FIRST : MI_OUT_W : MI_QK1_IN);
+  else if constexpr (FIRST) asm(MI_QK1_FIRST : MI_OUT_W : MI_QK1_IN);
+  else if constexpr (NOP) asm(MI_NOP MI_QK1_NEXT : MI_OUT_RW : MI_QK1_IN);
+  else asm(MI_QK1_NEXT : MI_OUT_RW : MI_QK1_IN);
+#undef MI_OUT_W
+#undef MI_OUT_RW
+}
+
+template <int J, int HS, bool FIRST, bool NOP>
+__device__ __forceinline__ void qk4(float (&s)[HS][4 / HS], const float (&q)[HS][4], const float (&k)[4]) {
+  if constexpr (HS == 2)
+    qk4_2<J, FIRST, NOP>(s, q, k);
+  else
+    qk4_1<J, FIRST, NOP>(s, q, k);
+}
+
+#undef MI_QK2_FIRST
+#undef MI_QK2_NEXT
+#undef MI_QK2_IN
+#undef MI_QK1_FIRST
+#undef MI_QK1_NEXT
+#undef MI_QK1_IN
+#undef MI_PV2
+#undef MI_PV1
+#undef MI_NOP
+#undef MI_DPP
+
+template <typename T>
+__device__ __forceinline__ T lds_load(const lds_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void lds_store(lds_t* p, T v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>(p) = v;
+}
+// 16 bytes per lane from r + voff into LDS at lds + 16 * lane.
+__device__ inline void dma16(rsrc_t r, lds_t* lds, unsigned voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
+}
+
+template <int D, typename KT, int HS, int NWV>
+struct DecodeCfg {
+  static constexpr int ELT = (int)sizeof(KT);
+  static constexpr int RB = D * ELT;              // bytes per cache row
+  static constexpr int NSLOT = RB / 16;           // 16-byte slots per row
+  static constexpr int SE = 16 / ELT;             // elements per slot
+  static constexpr int SUBB = kDecodeSub * RB;    // bytes of one K (or V) sub-tile
+  static constexpr int NDK = SUBB / 1024;         // 1 KB loads per K (or V) sub-tile
+  static constexpr int NDMA = 2 * NDK;
+  static constexpr int SLOTB = 2 * SUBB;          // ring slot: K rows, then V rows
+  static constexpr int NB0 = 128 * 1024 / (NWV * SLOTB);
+  static constexpr int NB = NB0 > 4 ? 4 : NB0;    // ring depth per wave
+  static constexpr int HSL = 4 * HS;              // head slots (G <= HSL)
+  static constexpr int DEPF = HSL * (D + 2);      // floats of one wave's deposit
+  static constexpr int REC = (DEPF + 3) & ~3;     // floats per record
+  static constexpr int NE = D / 64;               // float4 column blocks per lane
+  // LDS layout (bytes)
+  static constexpr int L_RING = 0;
+  static constexpr int L_DEP = L_RING + NWV * NB * SLOTB;
+  static constexpr int L_P = L_DEP + NWV * DEPF * 4;    // per wave: P[head slot][16]
+  static constexpr int L_FLAG = L_P + NWV * HSL * kDecodeSub * 4;
+  static constexpr int L_ITEMS = L_FLAG + 16;
+  static constexpr int L_TOTAL = L_ITEMS + kDecodeMaxItems * (int)sizeof(DecodeItem);
+  static_assert(sizeof(DecodeItem) % 16 == 0, "item table copied in 16-byte pieces");
+  static_assert(NB >= 2, "ring depth");
+  static_assert(SUBB % 1024 == 0, "1 KB load granularity");
+  static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
+  // vmcnt allowed while waiting for a slot's K (its V and the later slots may
+  // still be in flight) and for its V.
+  static constexpr int WAIT_K = NDK + NDMA * (NB - 1);
+  static constexpr int WAIT_V = NDMA * (NB - 1);
+  static_assert(WAIT_K <= 63, "vmcnt range");
+};
+
+// One workgroup per CU (the LDS ring fills it): NWV / 4 waves per SIMD.
+template <int D, typename KT, int HS, int NWV>
+__global__ __launch_bounds__(NWV* kWave) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
+void decode_kernel(const DecodeParams p) {
+  typedef DecodeCfg<D, KT, HS, NWV> C;
+  constexpr int HSL = C::HSL, NB = C::NB, NSLOT = C::NSLOT, NE = C::NE;
+  constexpr int NACC = 4 / HS;
+  constexpr bool F16 = C::ELT == 2;
+
+  extern __shared__ __attribute__((aligned(16))) char lds_dyn[];
+  lds_t* const lds = (lds_t*)lds_dyn;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int col = lane & 15;  // QK: position in the sub-tile; PV: column block
+  const int hb = lane >> 4;   // head slots hb + 4 h
+
+  // Records: one per workgroup, written and read with agent-coherent (sc1)
+  // 16-byte accesses through this resource.
+  const rsrc_t recr = make_rsrc(p.rec, (unsigned)(p.n_wg * C::REC * 4));
+
+  // Stage the item table (kernel arguments) in LDS; the whole table is copied
+  // so the loads do not wait for n_items.
   {
-    const float* q0 = reinterpret_cast<const float*>(reinterpret_cast<const char*>(it.q) +
-                                                     (int64_t)head0 * it.q_s1);
-    const int64_t q_s1f = it.q_s1 / 4;
+    constexpr int V16 = kDecodeMaxItems * (int)(sizeof(DecodeItem) / 16);
+    for (int i = threadIdx.x; i < V16; i += NWV * kWave)
+      lds_store<f32x4>(lds + C::L_ITEMS + 16 * i, reinterpret_cast<const f32x4*>(&p.item[0])[i]);
+    wg_barrier();
+  }
+  const lds_t* const tab = lds + C::L_ITEMS;
+
+  // This workgroup's item, group and share of the group's sub-tiles.
+  const int wg = blockIdx.x;
+  int ii = 0;
+  while (ii + 1 < p.n_items && wg >= uni(item_at(tab, ii + 1).wg0)) ++ii;
+  lds_item_t& it = item_at(tab, ii);
+  const int n_kv = uni(it.n_kv), spg = uni(it.spg), kpg = uni(it.kpg);
+  const char* const it_k = uni(it.k);
+  const char* const it_v = uni(it.v);
+  const float* const it_q = uni(it.q);
+  float* const it_out = uni(it.out);
+  const int64_t k_s1 = uni(it.k_s1), v_s1 = uni(it.v_s1), q_s1 = uni(it.q_s1), o_s1 = uni(it.o_s1);
+  const int local = wg - uni(it.wg0);
+  const int gl = local / kpg, part = local - gl * kpg;
+  const int g = gl / p.n_chunks, hc = gl - g * p.n_chunks;
+  const int G = p.n_rep / p.n_chunks;
+  const int head0 = g * p.n_rep + hc * G;
+  const int ks2 = (int)uni(it.k_s2), vs2 = (int)uni(it.v_s2);
+
+  // This lane's query elements for the DPP broadcast: qv[h][e][c] =
+  // Q[head0 + hb + 4h][64e + 4col + c] (head slots past G repeat head G-1 and
+  // are never written out). Requested before the first cache tile.
+  float qv[HS][NE][4];
+  {
+    const char* q0 = reinterpret_cast<const char*>(it_q) + (int64_t)head0 * q_s1;
 #pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int h = 0; h < HS; ++h)
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) qv[h][c] = q0[h * q_s1f + 16 * c + (lane & 15)];
+      for (int e = 0; e < NE; ++e) {
+        const int hs = min(hb + 4 * h, G - 1);
+        const f32x4 q4 = *reinterpret_cast<const f32x4*>(q0 + (int64_t)hs * q_s1 + 4 * (64 * e + 4 * col));
+        qv[h][e][0] = q4.x; qv[h][e][1] = q4.y; qv[h][e][2] = q4.z; qv[h][e][3] = q4.w;
+      }
   }
 
-  raw_t kb[NBUF][NK], vb[NBUF][NV];
-  // (the lane's base offset passes through an empty asm at every issue so the
-  // per-load offsets are formed next to their loads instead of being hoisted
-  // out of the loop, which would hold one register per load)
-  auto issue_k = [&](raw_t (&dst)[NK], int t) __attribute__((always_inline)) {
-    const rsrc_t r = t < t_end ? kres : none;
-    unsigned base = klane;
-    asm volatile("" : "+v"(base));
-    base += (unsigned)(t * kDecodeTile * ks2);
+  // DMA lane offsets: load i of a sub-tile fills LDS bytes [1024 i, +1024).
+  // K rows are swizzled (QK reads one row per lane); V rows are not (PV reads
+  // one whole row per wave, which is conflict-free as it lies).
+  unsigned offk[C::NDK], offv[C::NDK];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
-#pragma unroll
-      for (int i = 0; i < 16; ++i)
-        dst[c * 16 + i] = C::load(r, base + (unsigned)(i * 4 * ks2 + c * 64 * ELT));
-  };
-  auto issue_v = [&](raw_t (&dst)[NV], int t) __attribute__((always_inline)) {
-    const rsrc_t r = t < t_end ? vres : none;
-    unsigned base = vlane;
-    asm volatile("" : "+v"(base));
-    base += (unsigned)(t * kDecodeTile * vs2);
-#pragma unroll
-    for (int i = 0; i < NV; ++i) dst[i] = C::load(r, base + (unsigned)(i * RPI * vs2));
-  };
-#pragma unroll
-  for (int b = 0; b < NBUF; ++b) {
-    issue_k(kb[b], t_begin + b);
-    issue_v(vb[b], t_begin + b);
+  for (int i = 0; i < C::NDK; ++i) {
+    const int o = 1024 * i + 16 * lane;
+    const int r = o / C::RB;
+    const int j = ((o % C::RB) / 16) ^ swz<NSLOT>(r);
+    offk[i] = (unsigned)(r * ks2 + 16 * j);
+    offv[i] = (unsigned)(r * vs2 + o % C::RB);
   }
-
-  float m[G], l[G], acc[G][4];
+  lds_t* const ring = lds + C::L_RING + wv * NB * C::SLOTB;
+  // QK: logical slot j of this lane's row `col`.
+  const lds_t* kp[NSLOT];
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
+  for (int j = 0; j < NSLOT; ++j) kp[j] = ring + col * C::RB + 16 * (j ^ swz<NSLOT>(col));
+  // PV: this lane's dims 4 col + 64 e of row r, rows RB apart in the slot.
+  const lds_t* const vbase = ring + C::SUBB + 4 * col * C::ELT;
+  lds_t* const pw = lds + C::L_P + wv * (HSL * kDecodeSub * 4);  // this wave's P area
+
+  // Request stream: this workgroup's share [a, b) of the group's sub-tiles,
+  // taken round-robin by its waves (sub-tiles a + wv, a + wv + NWV, ...),
+  // through bounded resources advanced by pointer bumps.
+  const int a = (int)((int64_t)spg * part / kpg), b = (int)((int64_t)spg * (part + 1) / kpg);
+  const int n_v = b - a > wv ? (b - a - wv + NWV - 1) / NWV : 0;
+  const int gid = ii * p.n_head_kv * p.n_chunks + gl;
+  const rsrc_t none = make_rsrc(it_k, 0u);
+  const int row_first = kDecodeSub * (a + wv);
+  const char* rkp = it_k + (int64_t)g * k_s1 + (int64_t)row_first * ks2;
+  const char* rvp = it_v + (int64_t)g * v_s1 + (int64_t)row_first * vs2;
+  unsigned rkb = (unsigned)((n_kv - 1 - row_first) * ks2 + D * C::ELT);
+  unsigned rvb = (unsigned)((n_kv - 1 - row_first) * vs2 + D * C::ELT);
+  const int kstep = NWV * kDecodeSub * ks2, vstep = NWV * kDecodeSub * vs2;
+  int rk = 0;
+  auto refill = [&](lds_t* slot) __attribute__((always_inline)) {
+    rsrc_t kr = none, vr = none;
+    if (rk < n_v) {
+      kr = make_rsrc(rkp, rkb);
+      vr = make_rsrc(rvp, rvb);
+      rkp += kstep;
+      rvp += vstep;
+      rkb -= (unsigned)kstep;
+      rvb -= (unsigned)vstep;
+    }
+    ++rk;
+#pragma unroll
+    for (int i = 0; i < C::NDK; ++i) dma16(kr, slot + 1024 * i, offk[i]);
+#pragma unroll
+    for (int i = 0; i < C::NDK; ++i) dma16(vr, slot + C::SUBB + 1024 * i, offv[i]);
+  };
+#pragma unroll
+  for (int s = 0; s < NB; ++s) refill(ring + s * C::SLOTB);
+  // The queries were requested first; they are in registers once at most the
+  // ring's loads are outstanding (the empty asm makes the compiler wait here).
+#pragma unroll
+  for (int h = 0; h < HS; ++h)
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+      asm volatile("" : "+v"(qv[h][e][0]), "+v"(qv[h][e][1]), "+v"(qv[h][e][2]), "+v"(qv[h][e][3]));
+
+  float m[HS], l[HS], acc[HS][NE][4];
+#pragma unroll
+  for (int h = 0; h < HS; ++h) {
     m[h] = -INFINITY;
     l[h] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) acc[h][e] = 0.f;
+    for (int e = 0; e < NE; ++e)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) acc[h][e][jj] = 0.f;
   }
 
-  auto process = [&](raw_t (&kt)[NK], raw_t (&vt)[NV], int t) __attribute__((always_inline)) {
-    const int nvalid = min(kDecodeTile, n_kv - t * kDecodeTile);
+  // One sub-tile in ring slot SL (row0: its first position within the group).
+  auto process = [&](auto slc, int row0) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slc)::value;
+    constexpr int SOFF = SL * C::SLOTB;
+    wait_vmem<C::WAIT_K>();
 
-    // K tile to LDS: chunk c of row r is 256 contiguous bytes whose 16-byte
-    // slot s holds dims 64c + 4 (s ^ (r & 15)) .. +3, so lane r reading slot
-    // d of its own row hits 16 distinct bank groups across 16 lanes.
-    wave_lds_fence();
+    // K slots are requested up to KW ahead of their multiply-adds (LDS reads
+    // complete in order, so each block waits only for its own).
+    typedef typename std::conditional<F16, f16x8, f32x4>::type kvec_t;
+    constexpr int KW = NSLOT < 16 ? NSLOT : 16;
+    kvec_t kk[NSLOT];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+    for (int j = 0; j < KW; ++j) kk[j] = lds_load<kvec_t>(kp[j] + SOFF);
+    float s[HS][NACC];
+    static_for<0, NSLOT>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if constexpr (j + KW < NSLOT) kk[j + KW] = lds_load<kvec_t>(kp[j + KW] + SOFF);
+      if constexpr (!F16) {
+        const float kf[4] = {kk[j].x, kk[j].y, kk[j].z, kk[j].w};
+        float qs[HS][4];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int row = i * 4 + kr;
-        *reinterpret_cast<float4*>(&klds[c * CS + row * 64 + ((kc ^ (row & 15)) * 4)]) =
-            C::widen(kt[c * 16 + i]);
+        for (int h = 0; h < HS; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) qs[h][e] = qv[h][j >> 4][e];
+        qk4<j & 15, HS, j == 0, false>(s, qs, kf);
+      } else {
+        const float k0[4] = {(float)kk[j][0], (float)kk[j][1], (float)kk[j][2], (float)kk[j][3]};
+        const float k1[4] = {(float)kk[j][4], (float)kk[j][5], (float)kk[j][6], (float)kk[j][7]};
+        float q0[HS][4], q1[HS][4];
+#pragma unroll
+        for (int h = 0; h < HS; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            q0[h][e] = qv[h][(8 * j) >> 6][e];
+            q1[h][e] = qv[h][(8 * j + 4) >> 6][e];
+          }
+        qk4<(2 * j) & 15, HS, j == 0, true>(s, q0, k0);
+        qk4<(2 * j + 1) & 15, HS, false, true>(s, q1, k1);
       }
-    wave_lds_fence();
-    issue_k(kt, t + NBUF);  // the slot's K registers are free again
+    });
 
-    float s[NACC][G];
+    // Online softmax (base 2); the running max is uniform over a row.
+    const bool valid = row0 + col < n_kv;
+    float pr[HS];
 #pragma unroll
-    for (int a = 0; a < NACC; ++a)
+    for (int h = 0; h < HS; ++h) {
+      float x = s[h][0];
 #pragma unroll
-      for (int h = 0; h < G; ++h) s[a][h] = 0.f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const float* krow = klds + c * CS + lane * 64;
-#pragma unroll
-      for (int q16 = 0; q16 < 4; ++q16) {
-        // (qv passes through an empty asm so the broadcasts stay here instead
-        // of being hoisted out of the tile loop, which would need one
-        // register per broadcast value)
-        float qq[G];
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-          asm volatile("" : "+v"(qv[h][c * 4 + q16]));
-          qq[h] = qv[h][c * 4 + q16];
-        }
-        const float4 k0 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 0) ^ (lane & 15)) * 4]);
-        const float4 k1 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 1) ^ (lane & 15)) * 4]);
-        const float4 k2 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 2) ^ (lane & 15)) * 4]);
-        const float4 k3 = *reinterpret_cast<const float4*>(&krow[((4 * q16 + 3) ^ (lane & 15)) * 4]);
-        qk_step<0>(s, qq, k0.x);
-        qk_step<1>(s, qq, k0.y);
-        qk_step<2>(s, qq, k0.z);
-        qk_step<3>(s, qq, k0.w);
-        qk_step<4>(s, qq, k1.x);
-        qk_step<5>(s, qq, k1.y);
-        qk_step<6>(s, qq, k1.z);
-        qk_step<7>(s, qq, k1.w);
-        qk_step<8>(s, qq, k2.x);
-        qk_step<9>(s, qq, k2.y);
-        qk_step<10>(s, qq, k2.z);
-        qk_step<11>(s, qq, k2.w);
-        qk_step<12>(s, qq, k3.x);
-        qk_step<13>(s, qq, k3.y);
-        qk_step<14>(s, qq, k3.z);
-        qk_step<15>(s, qq, k3.w);
-      }
-    }
-
-    // Online softmax: wave-uniform running max per head, per-lane sums.
-    const bool valid = lane < nvalid;
-    float pv[8];
-#pragma unroll
-    for (int h = 0; h < 8; ++h) pv[h] = 0.f;
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float sh = s[0][h];
-#pragma unroll
-      for (int a = 1; a < NACC; ++a) sh += s[a][h];
-      const float x = valid ? sh * p.scale_log2e : -INFINITY;
-      const float mn = fmaxf(m[h], wave_max_dpp(x));
+      for (int t = 1; t < NACC; ++t) x += s[h][t];
+      x = valid ? x * p.scale_log2e : -INFINITY;
+      const float mn = fmaxf(m[h], row_max16(x));
       const float alpha = fast_exp2(m[h] - mn);
-      const float e = fast_exp2(x - mn);
-      l[h] = l[h] * alpha + e;
+      pr[h] = fast_exp2(x - mn);
+      l[h] = l[h] * alpha + pr[h];
       m[h] = mn;
-      pv[h] = e;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[h][j] *= alpha;
+      for (int e = 0; e < NE; ++e)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[h][e][jj] *= alpha;
     }
-
-    // Probabilities to LDS, [row][8], over the (now dead) K tile.
-    wave_lds_fence();
-    *reinterpret_cast<float4*>(&klds[lane * 8]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
-    if (G > 4)
-      *reinterpret_cast<float4*>(&klds[lane * 8 + 4]) = make_float4(pv[4], pv[5], pv[6], pv[7]);
-    wave_lds_fence();
-
-    // O += P.V (rows past n_kv loaded as zero and have P = 0).
+    // P[head slot][position] to this wave's LDS area; read back, each row's
+    // 16 probabilities broadcast to the 16 lanes of that row.
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int row = i * RPI + vr;
-      const float4 pa = *reinterpret_cast<const float4*>(&klds[row * 8]);
-      float4 pb = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (G > 4) pb = *reinterpret_cast<const float4*>(&klds[row * 8 + 4]);
-      const float pr[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
-      const float4 vv = C::widen(vt[i]);
+    for (int h = 0; h < HS; ++h) lds_store<float>(pw + 4 * ((hb + 4 * h) * kDecodeSub + col), pr[h]);
+    wave_lds_fence();
+    float pv[HS][kDecodeSub];
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        acc[h][0] = fmaf(pr[h], vv.x, acc[h][0]);
-        acc[h][1] = fmaf(pr[h], vv.y, acc[h][1]);
-        acc[h][2] = fmaf(pr[h], vv.z, acc[h][2]);
-        acc[h][3] = fmaf(pr[h], vv.w, acc[h][3]);
+    for (int h = 0; h < HS; ++h)
+#pragma unroll
+      for (int q4 = 0; q4 < kDecodeSub / 4; ++q4) {
+        const f32x4 t = lds_load<f32x4>(pw + 4 * ((hb + 4 * h) * kDecodeSub + 4 * q4));
+        pv[h][4 * q4 + 0] = t.x; pv[h][4 * q4 + 1] = t.y; pv[h][4 * q4 + 2] = t.z; pv[h][4 * q4 + 3] = t.w;
       }
-    }
-    issue_v(vt, t + NBUF);
+
+    wait_vmem<C::WAIT_V>();
+    typedef typename std::conditional<F16, half4_t, f32x4>::type vvec_t;
+#pragma unroll
+    for (int r = 0; r < kDecodeSub; ++r)
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        const vvec_t v4 = lds_load<vvec_t>(vbase + SOFF + r * C::RB + 64 * e * C::ELT);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+          for (int h = 0; h < HS; ++h) acc[h][e][jj] = fmaf(pv[h][r], (float)v4[jj], acc[h][e][jj]);
+      }
+    wave_lds_fence();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot reads done before it is refilled
+    refill(ring + SOFF);
   };
 
-  // Slots are used in turn; exits leave the loop rather than re-entering it,
-  // so the wait counts at the loop head see one pattern of loads in flight.
-  int t = t_begin;
-  while (true) {
-    process(kb[0], vb[0], t);
-    if (++t >= t_end) break;
-    if (NBUF > 1) {
-      process(kb[NBUF - 1], vb[NBUF - 1], t);
-      if (++t >= t_end) break;
+  // Ring slots are used in turn; each case falls through to the next slot.
+  int row0 = row_first;
+  for (int k = 0; k < n_v;) {
+    switch (k & (NB - 1)) {
+      case 0:
+        process(std::integral_constant<int, 0>{}, row0);
+        row0 += NWV * kDecodeSub;
+        if (++k >= n_v) break;
+        [[fallthrough]];
+      case 1:
+        process(std::integral_constant<int, 1>{}, row0);
+        row0 += NWV * kDecodeSub;
+        if (++k >= n_v) break;
+        if constexpr (NB == 2) break;
+        [[fallthrough]];
+      case 2:
+        if constexpr (NB > 2) {
+          process(std::integral_constant<int, (NB > 2 ? 2 : 0)>{}, row0);
+          row0 += NWV * kDecodeSub;
+          if (++k >= n_v) break;
+        }
+        [[fallthrough]];
+      default:
+        if constexpr (NB > 3) {
+          process(std::integral_constant<int, (NB > 3 ? 3 : 0)>{}, row0);
+          row0 += NWV * kDecodeSub;
+          ++k;
+        }
+        break;
     }
   }
 
-  // Wave totals: l over all lanes, acc over the RPI lanes sharing a column.
+  // The waves meet in LDS.
+  float* const dep = reinterpret_cast<float*>(lds_dyn + C::L_DEP);
 #pragma unroll
-  for (int h = 0; h < G; ++h) {
-    l[h] = wave_sum(l[h]);
+  for (int h = 0; h < HS; ++h) l[h] = row_sum16(l[h]);
+  {
+    float* dw = dep + wv * C::DEPF;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int h = 0; h < HS; ++h) {
 #pragma unroll
-      for (int off = LPR; off < kWave; off <<= 1) acc[h][j] += __shfl_xor(acc[h][j], off, kWave);
-    }
-  }
-
-  if (it.nw == 1) {  // the run is the whole group
-    if (lane < LPR) {
-#pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float inv = 1.f / l[h];
-        float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) +
-                                            (int64_t)(head0 + h) * it.o_s1);
-        *reinterpret_cast<float4*>(o + 4 * lane) =
-            make_float4(acc[h][0] * inv, acc[h][1] * inv, acc[h][2] * inv, acc[h][3] * inv);
+      for (int e = 0; e < NE; ++e)
+        *reinterpret_cast<f32x4*>(dw + (hb + 4 * h) * D + 64 * e + 4 * col) =
+            f32x4{acc[h][e][0], acc[h][e][1], acc[h][e][2], acc[h][e][3]};
+      if (col == 0) {
+        dw[HSL * D + 2 * (hb + 4 * h)] = m[h];
+        dw[HSL * D + 2 * (hb + 4 * h) + 1] = l[h];
       }
     }
-    return;
   }
-  float* rec = p.part + (int64_t)wid * REC;
-  if (lane == 0) {
+  wg_barrier();
+  {
+    // wave wv combines head slots wv + NWV t; lane = (slot t, float4 cq)
+    constexpr int SPW = (HSL + NWV - 1) / NWV;  // head slots per wave
+    const int t = lane / (D / 4), cq = lane % (D / 4);
+    const int hs = wv + NWV * t;
+    if (t < SPW && hs < HSL) {
+      float mx = -INFINITY;
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      rec[h] = m[h];
-      rec[G + h] = l[h];
+      for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, dep[w * C::DEPF + HSL * D + 2 * hs]);
+      float lt = 0.f;
+      f32x4 at = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        const float* dw = dep + w * C::DEPF;
+        const float mw = dw[HSL * D + 2 * hs];
+        const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);  // a wave with no sub-tile
+        lt += wt * dw[HSL * D + 2 * hs + 1];
+        at += wt * *reinterpret_cast<const f32x4*>(dw + hs * D + 4 * cq);
+      }
+      if (kpg == 1) {
+        if (hs < G) {
+          float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) +
+                                              (int64_t)(head0 + hs) * o_s1);
+          *reinterpret_cast<f32x4*>(o + 4 * cq) = at * (1.f / lt);
+        }
+      } else {
+        const unsigned r0 = (unsigned)(wg * C::REC * 4);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, at), recr,
+                                               r0 + 4 * (hs * D + 4 * cq), 0, kSc1);
+        if (cq == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{mx, lt}), recr,
+                                                r0 + 4 * (HSL * D + 2 * hs), 0, kSc1);
+      }
     }
   }
-  if (lane < LPR) {
+  wait_vmem<0>();  // no LDS DMA outlives the workgroup; record stores have completed
+  if (kpg == 1) return;
+
+  // Cross-workgroup combine by the group's last arriving workgroup.
+  wg_barrier();
+  unsigned* flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
+  if (threadIdx.x == 0) {
+    const unsigned old =
+        __hip_atomic_fetch_add(p.cnt + gid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    flag[0] = old == (unsigned)(kpg - 1) ? 1u : 0u;
+  }
+  wg_barrier();
+  if (!__builtin_amdgcn_readfirstlane(flag[0])) return;
+
+  constexpr int NP = HSL * D / 4;             // (head slot, float4) pairs
+  constexpr int NSUB = NWV * kWave / NP;      // record subsets
+  static_assert(NSUB >= 1, "one pair per thread");
+  constexpr int RB8 = 8;                      // records per subset requested at once
+  const int tt = threadIdx.x;
+  const int pair = tt % NP, sub = tt / NP;
+  const int hs = pair / (D / 4), cq = pair % (D / 4);
+  const unsigned rec0 = (unsigned)((wg - part) * C::REC * 4);  // the group's first record (bytes)
+  float mx = -INFINITY, lt = 0.f;
+  f32x4 at = {0.f, 0.f, 0.f, 0.f};
+  if (sub < NSUB) {
+    for (int r0 = sub; r0 < kpg; r0 += RB8 * NSUB) {
+      float mr[RB8], lr[RB8];
+      f32x4 ar[RB8];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-      *reinterpret_cast<float4*>(&rec[HDR + h * D + 4 * lane]) =
-          make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      for (int i = 0; i < RB8; ++i) {  // clamped indices: every load is issued, extras weigh 0
+        const unsigned rb = rec0 + (unsigned)(min(r0 + i * NSUB, kpg - 1) * C::REC * 4);
+        const f32x2 ml = __builtin_bit_cast(
+            f32x2, __builtin_amdgcn_raw_buffer_load_b64(recr, rb + 4 * (HSL * D + 2 * hs), 0, kSc1));
+        mr[i] = ml.x;
+        lr[i] = ml.y;
+        ar[i] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(recr, rb + 4 * (hs * D + 4 * cq), 0, kSc1));
+      }
+#pragma unroll
+      for (int i = 0; i < RB8; ++i) {
+        const float mi = r0 + i * NSUB < kpg ? mr[i] : -INFINITY;
+        const float mn = fmaxf(mx, mi);
+        const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+        const float wn = mi == -INFINITY ? 0.f : fast_exp2(mi - mn);
+        lt = lt * wo + lr[i] * wn;
+        at = at * wo + ar[i] * wn;
+        mx = mn;
+      }
+    }
   }
-}
-
-template <int D, typename KT, int G>
-__global__ __launch_bounds__(kWave) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_kernel(const DecodeParams p) {
-  decode_body<D, KT, G, 1>(p);
-}
-
-template <int D, typename KT, int G>
-__global__ __launch_bounds__(kWave) void decode_kernel_deep(const DecodeParams p) {
-  decode_body<D, KT, G, 2>(p);
-}
-
-// Combines the nw run records of one (group, head) per workgroup. Thread t
-// owns output dims 4 (t % (D/4)) .. +3 and the records s = t / (D/4) + k*RS:
-// it keeps a running (m, l, acc) over its few records (all loads independent,
-// so one memory round trip), then the RS partials of each dim combine through
-// LDS with the same stable rescaling.
-template <int D, int G>
-__global__ __launch_bounds__(256) void decode_merge_kernel(const DecodeParams p) {
-  constexpr int HDR = record_header(G);
-  constexpr int REC = HDR + G * D;
-  constexpr int C4 = D / 4;          // threads per record (one float4 of dims each)
-  constexpr int RS = 256 / C4;       // record subsets
-  __shared__ float sm[RS], sl[RS];
-  __shared__ float4 sa[RS][C4];
-  const int per_item = p.n_head_kv * p.n_chunks;
-  const int grp = blockIdx.x / G;
-  const int h = blockIdx.x % G;
-  const DecodeItem& it = p.item[grp / per_item];
-  const int S = it.nw;
-  if (S == 1) return;  // written by its only run
-  const int gl = grp % per_item;
-  const int g = gl / p.n_chunks;
-  const int hc = gl % p.n_chunks;
-  const int head = g * p.n_rep + hc * G + h;
-  const float* base = p.part + (int64_t)(it.wave0 + gl * S) * REC;
-  const int c4 = threadIdx.x % C4, sub = threadIdx.x / C4;
-
-  float m = -INFINITY, l = 0.f;
-  float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 4
-  for (int s = sub; s < S; s += RS) {
-    const float* r = base + (int64_t)s * REC;
-    const float ms = r[h], ls = r[G + h];
-    const float4 as = *reinterpret_cast<const float4*>(r + HDR + h * D + 4 * c4);
-    const float mn = fmaxf(m, ms);
-    const float wo = fast_exp2(m - mn), wn = fast_exp2(ms - mn);
-    l = l * wo + ls * wn;
-    a.x = a.x * wo + as.x * wn;
-    a.y = a.y * wo + as.y * wn;
-    a.z = a.z * wo + as.z * wn;
-    a.w = a.w * wo + as.w * wn;
-    m = mn;
+  if constexpr (NSUB > 1) {
+    float* tmp = reinterpret_cast<float*>(lds_dyn + C::L_RING);  // the ring is drained
+    if (sub < NSUB) {
+      tmp[(sub * NP + pair) * 6 + 0] = mx;
+      tmp[(sub * NP + pair) * 6 + 1] = lt;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) tmp[(sub * NP + pair) * 6 + 2 + jj] = at[jj];
+    }
+    wg_barrier();
+    if (sub == 0) {
+#pragma unroll
+      for (int s2 = 1; s2 < NSUB; ++s2) {
+        const float* e = tmp + (s2 * NP + pair) * 6;
+        const float mn = fmaxf(mx, e[0]);
+        const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+        const float wn = e[0] == -INFINITY ? 0.f : fast_exp2(e[0] - mn);
+        lt = lt * wo + e[1] * wn;
+        at = at * wo + f32x4{e[2], e[3], e[4], e[5]} * wn;
+        mx = mn;
+      }
+    }
   }
-  if (c4 == 0) {
-    sm[sub] = m;
-    sl[sub] = l;
+  if (sub == 0 && hs < G) {
+    float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
+    *reinterpret_cast<f32x4*>(o + 4 * cq) = at * (1.f / lt);
   }
-  sa[sub][c4] = a;
-  __syncthreads();
-  if (sub != 0) return;
-  float mx = -INFINITY;
-  for (int k = 0; k < RS; ++k) mx = fmaxf(mx, sm[k]);
-  float lt = 0.f;
-  float4 at = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int k = 0; k < RS; ++k) {
-    const float wk = sm[k] == -INFINITY ? 0.f : fast_exp2(sm[k] - mx);  // subset with no record
-    lt += wk * sl[k];
-    const float4 ak = sa[k][c4];
-    at.x += wk * ak.x;
-    at.y += wk * ak.y;
-    at.z += wk * ak.z;
-    at.w += wk * ak.w;
-  }
-  const float inv = 1.f / lt;
-  float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it.out) + (int64_t)head * it.o_s1);
-  *reinterpret_cast<float4*>(o + 4 * c4) = make_float4(at.x * inv, at.y * inv, at.z * inv, at.w * inv);
+  if (tt == 0) __hip_atomic_store(p.cnt + gid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Depth 1 (two waves per SIMD) for head_dim 64; head_dim 128 tiles do not fit
-// 256 registers with a refill in flight, so they run at depth 2 (one wave per
-// SIMD). MI_HIP_DECODE_DEPTH=1|2 overrides (tuning).
-int decode_depth(int head_dim) {
-  static const int forced = [] {
-    const char* e = std::getenv("MI_HIP_DECODE_DEPTH");
-    return e && (e[0] == '1' || e[0] == '2') ? e[0] - '0' : 0;
-  }();
-  return forced ? forced : (head_dim == 64 ? 1 : 2);
+// Waves per workgroup: two per SIMD at head_dim 64 (a 128 KB ring still gives
+// every wave two slots), one per SIMD at head_dim 128.
+template <int D, typename KT>
+constexpr int decode_waves() {
+  return D == 64 ? 8 : 4;
 }
 
-template <int D, typename KT, int G>
-static hipError_t launch_decode_t(const DecodeParams& p, int max_nw, hipStream_t stream) {
-  if (decode_depth(D) == 2)
-    hipLaunchKernelGGL((decode_kernel_deep<D, KT, G>), dim3((unsigned)p.n_waves), dim3(kWave), 0,
-                       stream, p);
-  else
-    hipLaunchKernelGGL((decode_kernel<D, KT, G>), dim3((unsigned)p.n_waves), dim3(kWave), 0,
-                       stream, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || max_nw <= 1) return e;
-  const unsigned groups = (unsigned)(p.n_items * p.n_head_kv * p.n_chunks);
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(groups * G), dim3(256), 0, stream, p);
+template <int D, typename KT, int HS>
+static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+  constexpr int NWV = decode_waves<D, KT>();
+  typedef DecodeCfg<D, KT, HS, NWV> C;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, KT, HS, NWV>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, C::L_TOTAL);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV>), dim3((unsigned)p.n_wg), dim3(NWV * kWave),
+                     C::L_TOTAL, stream, p);
   return hipGetLastError();
 }
 
 template <int D, typename KT>
-static hipError_t launch_decode_g(const DecodeParams& p, int g, int max_nw, hipStream_t stream) {
-  switch (g) {
-    case 1: return launch_decode_t<D, KT, 1>(p, max_nw, stream);
-    case 2: return launch_decode_t<D, KT, 2>(p, max_nw, stream);
-    case 4: return launch_decode_t<D, KT, 4>(p, max_nw, stream);
-    case 7: return launch_decode_t<D, KT, 7>(p, max_nw, stream);
-    case 8: return launch_decode_t<D, KT, 8>(p, max_nw, stream);
-    default: return hipErrorInvalidValue;
-  }
+static hipError_t launch_decode_h(const DecodeParams& p, int group, hipStream_t stream) {
+  return group > 4 ? launch_decode_t<D, KT, 2>(p, stream) : launch_decode_t<D, KT, 1>(p, stream);
 }
 
+int decode_wg_waves(int head_dim) { return head_dim == 64 ? 8 : 4; }
+
 int decode_group_size(int n_rep) {
-  static const int kSizes[] = {8, 7, 4, 2, 1};
+  static const int kSizes[] = {8, 7, 6, 5, 4, 3, 2, 1};
   for (int g : kSizes)
     if (n_rep % g == 0) return g;
   return 1;
 }
 
 size_t decode_record_floats(int head_dim, int group) {
-  return (size_t)record_header(group) + (size_t)group * head_dim;
+  const int hsl = group > 4 ? 8 : 4;
+  return (size_t)((hsl * (head_dim + 2) + 3) & ~3);
 }
 
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, int max_nw,
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
                          hipStream_t stream) {
   if (head_dim == 64)
-    return f16 ? launch_decode_g<64, _Float16>(p, group, max_nw, stream)
-               : launch_decode_g<64, float>(p, group, max_nw, stream);
+    return f16 ? launch_decode_h<64, _Float16>(p, group, stream)
+               : launch_decode_h<64, float>(p, group, stream);
   if (head_dim == 128)
-    return f16 ? launch_decode_g<128, _Float16>(p, group, max_nw, stream)
-               : launch_decode_g<128, float>(p, group, max_nw, stream);
+    return f16 ? launch_decode_h<128, _Float16>(p, group, stream)
+               : launch_decode_h<128, float>(p, group, stream);
   return hipErrorInvalidValue;
 }
 

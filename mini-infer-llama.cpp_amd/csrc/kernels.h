@@ -11,11 +11,12 @@
 namespace mi {
 
 // decode.hip
-int decode_group_size(int n_rep);                       // G: Q heads per wave group
-int decode_depth(int head_dim);                         // K/V tiles in flight per wave (1, 2)
-size_t decode_record_floats(int head_dim, int group);   // floats per split partial
-// max_nw: the largest runs-per-group of any item (1: no merge launch).
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, int max_nw,
+int decode_group_size(int n_rep);                       // G: Q heads per group
+int decode_wg_waves(int head_dim);                      // waves per decode workgroup
+size_t decode_record_floats(int head_dim, int group);   // floats per cross-workgroup record
+// p.rec / p.cnt: one record per workgroup and the per-group arrival counters
+// (zero on entry, left zero on exit).
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
                          hipStream_t stream);
 
 // prefill.hip

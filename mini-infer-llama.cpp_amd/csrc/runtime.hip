@@ -95,10 +95,14 @@ int bind_device() {
   return MI_HIP_OK;
 }
 
-// Grows the workspace to at least `bytes` of partials. Growth synchronises the
-// device first, so no in-flight kernel still uses the old buffer.
-int ensure_workspace(size_t part_bytes) {
-  const size_t need = std::max<size_t>(256, (part_bytes + 255) & ~size_t(255));
+// Workspace layout: the decode arrival counters (kCounterBytes, zero between
+// launches), then the decode records. Grows to at least `rec_bytes` of records;
+// growth synchronises the device first, so no in-flight kernel still uses the
+// old buffer, and the new counters start at zero.
+constexpr size_t kCounterBytes = 64 * 1024;
+
+int ensure_workspace(size_t rec_bytes) {
+  const size_t need = kCounterBytes + ((rec_bytes + 255) & ~size_t(255));
   std::lock_guard<std::mutex> lk(g.mu);
   if (g.ws && g.ws_bytes >= need) return MI_HIP_OK;
   if (g.ws) {
@@ -110,12 +114,19 @@ int ensure_workspace(size_t part_bytes) {
   void* p = nullptr;
   int rc = dev_alloc(&p, need, "workspace");
   if (rc) return rc;
+  hipError_t e = hipMemset(p, 0, kCounterBytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    dev_free(p, need);
+    return hip_fail(e, "workspace init");
+  }
   g.ws = static_cast<char*>(p);
   g.ws_bytes = need;
   return MI_HIP_OK;
 }
 
-float* ws_part() { return reinterpret_cast<float*>(g.ws); }
+unsigned* ws_counters() { return reinterpret_cast<unsigned*>(g.ws); }
+float* ws_records() { return reinterpret_cast<float*>(g.ws + kCounterBytes); }
 
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
@@ -127,52 +138,48 @@ int env_int(const char* name, int dflt) {
 // ---------------------------------------------------------------------------
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Waves a decode launch aims for: as many as the SIMDs hold at once (two per
-// SIMD at depth 1, one at depth 2).
-int decode_wave_target(int head_dim) {
-  const int forced = env_int("MI_HIP_DECODE_WAVES", 0);
-  return forced > 0 ? forced : std::max(1, 4 * g.n_cu * (mi::decode_depth(head_dim) == 2 ? 1 : 2));
-}
-
+// Decode launch plan. Every group (item, KV head, head chunk) gets kpg
+// workgroups, in proportion to its share of the launch's sub-tiles so that the
+// launch has about one workgroup per CU; at least one, and no more than leave
+// each wave a sub-tile. MI_HIP_DECODE_KPG=n forces kpg (tuning).
 struct DecodePlan {
   int group = 1, n_chunks = 1;
-  int n_waves = 0, max_nw = 1;
-  size_t part_floats = 0;
+  int n_wg = 0;
 };
 
-// Runs per group for each item: about `decode_wave_target()` waves in total,
-// shared out in proportion to the items' tile counts, each run at least one
-// 64-position tile. Fills wave0/nw of the items.
 DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim) {
   DecodePlan p;
   p.group = mi::decode_group_size(n_rep);
   p.n_chunks = n_rep / p.group;
-  const int per_item = n_head_kv * p.n_chunks;
-  int64_t tiles = 0;
-  for (int i = 0; i < n_items; ++i)
-    tiles += (int64_t)per_item * ((it[i].n_kv + mi::kDecodeTile - 1) / mi::kDecodeTile);
-  const int64_t target = decode_wave_target(head_dim);
-  int64_t waves = 0;
+  const int gpi = n_head_kv * p.n_chunks;
+  const int waves = mi::decode_wg_waves(head_dim);
+  int64_t sub = 0;
   for (int i = 0; i < n_items; ++i) {
-    const int64_t tpg = (it[i].n_kv + mi::kDecodeTile - 1) / mi::kDecodeTile;
-    const int nw = (int)std::max<int64_t>(1, std::min<int64_t>(tpg, tpg * target / tiles));
-    it[i].wave0 = (int32_t)waves;
-    it[i].nw = nw;
-    waves += (int64_t)per_item * nw;
-    p.max_nw = std::max(p.max_nw, nw);
+    it[i].spg = (it[i].n_kv + mi::kDecodeSub - 1) / mi::kDecodeSub;
+    sub += (int64_t)gpi * it[i].spg;
   }
-  p.n_waves = (int)waves;
-  p.part_floats = p.max_nw > 1 ? (size_t)waves * mi::decode_record_floats(head_dim, p.group) : 0;
+  const int forced = env_int("MI_HIP_DECODE_KPG", 0);
+  int64_t wg = 0;
+  for (int i = 0; i < n_items; ++i) {
+    const int64_t cap = std::max<int64_t>(1, (it[i].spg + waves - 1) / waves);
+    int64_t k = forced > 0 ? forced : (int64_t)g.n_cu * it[i].spg / std::max<int64_t>(1, sub);
+    k = std::max<int64_t>(1, std::min<int64_t>(k, cap));
+    it[i].kpg = (int32_t)k;
+    it[i].wg0 = (int32_t)wg;
+    wg += (int64_t)gpi * k;
+  }
+  p.n_wg = (int)wg;
   return p;
 }
 
-// Records for any decode launch of up to kDecodeMaxItems items of this shape:
-// the proportional shares sum to at most the target, plus one per group for
-// the at-least-one rounding.
-size_t decode_part_bound(int n_head_kv, int n_rep, int head_dim) {
+// Record bytes that cover every decode launch of this shape: at most one
+// workgroup per CU plus one per group for the at-least-one rounding.
+size_t decode_rec_bound(int n_head_kv, int n_rep, int head_dim) {
   const int group = mi::decode_group_size(n_rep);
   const int64_t groups = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group);
-  return (size_t)(decode_wave_target(head_dim) + groups) * mi::decode_record_floats(head_dim, group);
+  const int forced = env_int("MI_HIP_DECODE_KPG", 0);
+  const int64_t wgs = forced > 0 ? groups * forced : g.n_cu + groups;
+  return (size_t)wgs * mi::decode_record_floats(head_dim, group) * sizeof(float);
 }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -299,32 +306,46 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
   int rc = resolve_kv(&items[0], &r0);
   if (rc) return rc;
   const int elt = r0.f16 ? 2 : 4;
-  for (int base = 0; base < n; base += mi::kDecodeMaxItems) {
-    const int cnt = std::min(mi::kDecodeMaxItems, n - base);
+  const int gpi = r0.n_head_kv * (items[0].n_rep / mi::decode_group_size(items[0].n_rep));
+  if ((size_t)mi::kDecodeMaxItems * gpi * sizeof(unsigned) > kCounterBytes)
+    return fail(MI_HIP_E_UNSUPPORTED, "too many heads for one decode launch (%d groups per item)",
+                gpi);
+  // Launches of up to kDecodeMaxItems consecutive items sharing the position
+  // strides (the kernel's per-lane load offsets derive from them).
+  int base = 0;
+  while (base < n) {
     mi::DecodeParams p{};
-    for (int i = 0; i < cnt; ++i) {
+    int cnt = 0;
+    for (; cnt < mi::kDecodeMaxItems && base + cnt < n; ++cnt) {
       Resolved r;
-      rc = resolve_kv(&items[base + i], &r);
+      rc = resolve_kv(&items[base + cnt], &r);
       if (rc) return rc;
-      p.item[i] = make_item(&items[base + i], r);
-      // the kernel addresses one KV head's rows with 32-bit byte offsets
-      const int64_t last = (int64_t)(p.item[i].n_kv - 1);
+      if (cnt > 0 && (r.k_s2 != p.item[0].k_s2 || r.v_s2 != p.item[0].v_s2)) break;
+      if (r.k_s2 < (int64_t)r.head_dim * elt || r.v_s2 < (int64_t)r.head_dim * elt)
+        return fail(MI_HIP_E_UNSUPPORTED, "item %d: position stride below one row", base + cnt);
+      p.item[cnt] = make_item(&items[base + cnt], r);
+      // one group's rows are addressed with 32-bit byte offsets
+      const int64_t last = (int64_t)(p.item[cnt].n_kv - 1);
       if (last * r.k_s2 + (int64_t)r.head_dim * elt > INT32_MAX ||
           last * r.v_s2 + (int64_t)r.head_dim * elt > INT32_MAX)
         return fail(MI_HIP_E_UNSUPPORTED,
-                    "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + i);
+                    "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + cnt);
     }
     const DecodePlan plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim);
-    if ((rc = ensure_workspace(plan.part_floats * sizeof(float)))) return rc;
+    const size_t rec_bytes =
+        (size_t)plan.n_wg * mi::decode_record_floats(r0.head_dim, plan.group) * sizeof(float);
+    if ((rc = ensure_workspace(rec_bytes))) return rc;
     p.n_items = cnt;
     p.n_rep = items[0].n_rep;
     p.n_head_kv = r0.n_head_kv;
     p.n_chunks = plan.n_chunks;
-    p.n_waves = plan.n_waves;
+    p.n_wg = plan.n_wg;
     p.scale_log2e = items[0].scale * kLog2e;
-    p.part = ws_part();
-    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, plan.max_nw, stream);
+    p.rec = ws_records();
+    p.cnt = ws_counters();
+    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
+    base += cnt;
   }
   return MI_HIP_OK;
 }
@@ -356,7 +377,7 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
 
 // Workspace bytes that cover every decode call on this cache (prefill needs none).
 size_t workspace_for(const mi_hip_kv_desc& d) {
-  return decode_part_bound(d.n_head_kv, d.n_head / d.n_head_kv, d.head_dim) * sizeof(float);
+  return decode_rec_bound(d.n_head_kv, d.n_head / d.n_head_kv, d.head_dim);
 }
 
 // ---------------------------------------------------------------------------
