@@ -28,15 +28,15 @@ struct DecodeItem {
   int64_t q_s1;        // Q: bytes between heads
   int64_t o_s1;        // O: bytes between heads
   int32_t n_kv;        // keys [0, n_kv) are visible
-  int32_t spg;         // sub-tiles per group: ceil(n_kv / kDecodeSub)
+  int32_t spg;         // sub-tiles per group, ceil(n_kv / kDecodeSub) (host planning)
   int32_t wg0;         // first workgroup of this item
   int32_t kpg;         // workgroups per group
 };
 
 // Work decomposition. A group is (item, KV head g, head chunk hc): the G Q
 // heads g*n_rep + hc*G .. + G - 1 that read KV head g. Each group is served by
-// kpg workgroups of its item; workgroup wg0 + gl*kpg + part owns sub-tiles
-// [spg*part/kpg, spg*(part+1)/kpg) of the item's group gl and leaves one
+// kpg workgroups of its item; workgroup wg0 + gl*kpg + part owns positions
+// [n_kv*part/kpg, n_kv*(part+1)/kpg) of the item's group gl and leaves one
 // record when kpg > 1.
 struct DecodeParams {
   DecodeItem item[kDecodeMaxItems];

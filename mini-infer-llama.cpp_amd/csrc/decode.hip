@@ -7,17 +7,19 @@
 // Q heads that read KV head g (GQA is an index mapping: every K/V row is read
 // once for all G heads, never copied). Each group is served by kpg workgroups
 // (the host sizes kpg so the launch has about one workgroup per CU); workgroup
-// part p owns a contiguous share of the group's 16-position sub-tiles, and its
-// NWV waves take the share's sub-tiles round-robin. A workgroup never changes
-// group, so its waves never meet before the end.
+// part p owns the contiguous share [n_kv p / kpg, n_kv (p + 1) / kpg) of the
+// group's positions, cut into sub-tiles of 16 positions (the last one
+// partial) that its NWV waves take one at a time from an LDS counter, so the
+// waves finish together however unevenly memory serves them. A workgroup
+// never changes group, so its waves never meet before the end.
 //
 // Streaming. Each wave owns an LDS ring of NB slots; a slot holds one
 // sub-tile's K rows then its V rows, written by buffer_load ... lds (direct to
-// LDS, no registers). Every refill is issued -- past the wave's last sub-tile
-// through a zero-sized resource that reads nothing -- so the number of loads
+// LDS, no registers). Every refill is issued -- past the share's last
+// sub-tile through a zero-sized resource that reads nothing -- so the number of loads
 // issued after any slot's K (or V) is always the same and the waits are fixed
-// vmcnt values. Rows past n_kv lie outside the group's bounded resource and
-// arrive as zeros. The 16-byte slots of each K row are stored XOR-swizzled by
+// vmcnt values. Rows past the share lie outside the sub-tile's bounded
+// resource and arrive as zeros without a memory request. The 16-byte slots of each K row are stored XOR-swizzled by
 // row, so the lane-per-row reads below are free of bank conflicts.
 //
 // Per sub-tile (lane = (row r = lane / 16, column i = lane % 16)):
@@ -271,16 +273,21 @@ void decode_kernel(const DecodeParams p) {
     constexpr int V16 = kDecodeMaxItems * (int)(sizeof(DecodeItem) / 16);
     for (int i = threadIdx.x; i < V16; i += NWV * kWave)
       lds_store<f32x4>(lds + C::L_ITEMS + 16 * i, reinterpret_cast<const f32x4*>(&p.item[0])[i]);
+    if (threadIdx.x == 0) lds_store<unsigned>(lds + C::L_FLAG + 4, 0u);  // sub-tile take counter
     wg_barrier();
   }
   const lds_t* const tab = lds + C::L_ITEMS;
 
-  // This workgroup's item, group and share of the group's sub-tiles.
+  // This workgroup's item: the number of items after the first whose first
+  // workgroup is at or below this one (one LDS read per lane and a ballot).
   const int wg = blockIdx.x;
-  int ii = 0;
-  while (ii + 1 < p.n_items && wg >= uni(item_at(tab, ii + 1).wg0)) ++ii;
+  int ii;
+  {
+    const int w0 = item_at(tab, lane & (kDecodeMaxItems - 1)).wg0;
+    ii = __popcll(__ballot(lane >= 1 && lane < p.n_items && wg >= w0));
+  }
   lds_item_t& it = item_at(tab, ii);
-  const int n_kv = uni(it.n_kv), spg = uni(it.spg), kpg = uni(it.kpg);
+  const int n_kv = uni(it.n_kv), kpg = uni(it.kpg);
   const char* const it_k = uni(it.k);
   const char* const it_v = uni(it.v);
   const float* const it_q = uni(it.q);
@@ -330,38 +337,43 @@ void decode_kernel(const DecodeParams p) {
   const lds_t* const vbase = ring + C::SUBB + 4 * col * C::ELT;
   lds_t* const pw = lds + C::L_P + wv * (HSL * kDecodeSub * 4);  // this wave's P area
 
-  // Request stream: this workgroup's share [a, b) of the group's sub-tiles,
-  // taken round-robin by its waves (sub-tiles a + wv, a + wv + NWV, ...),
-  // through bounded resources advanced by pointer bumps.
-  const int a = (int)((int64_t)spg * part / kpg), b = (int)((int64_t)spg * (part + 1) / kpg);
-  const int n_v = b - a > wv ? (b - a - wv + NWV - 1) / NWV : 0;
+  // Request stream: this workgroup's share [a, b) of the group's positions in
+  // sub-tiles of 16 (the last one partial). The waves take the sub-tiles in
+  // turn from a workgroup counter in LDS as they refill their slots, so a wave
+  // that is served faster takes more and the waves finish together. Rows past
+  // b lie outside the sub-tile's bounded resource and arrive as zeros without
+  // a memory request; a take past the share refills through a zero-sized
+  // resource. rows[s]: first position of the sub-tile in ring slot s, or -1.
+  const int a = (int)((int64_t)n_kv * part / kpg), b = (int)((int64_t)n_kv * (part + 1) / kpg);
+  const unsigned nsub = (unsigned)((b - a + kDecodeSub - 1) / kDecodeSub);
   const int gid = ii * p.n_head_kv * p.n_chunks + gl;
   const rsrc_t none = make_rsrc(it_k, 0u);
-  const int row_first = kDecodeSub * (a + wv);
-  const char* rkp = it_k + (int64_t)g * k_s1 + (int64_t)row_first * ks2;
-  const char* rvp = it_v + (int64_t)g * v_s1 + (int64_t)row_first * vs2;
-  unsigned rkb = (unsigned)((n_kv - 1 - row_first) * ks2 + D * C::ELT);
-  unsigned rvb = (unsigned)((n_kv - 1 - row_first) * vs2 + D * C::ELT);
-  const int kstep = NWV * kDecodeSub * ks2, vstep = NWV * kDecodeSub * vs2;
-  int rk = 0;
-  auto refill = [&](lds_t* slot) __attribute__((always_inline)) {
+  const char* const kg = it_k + (int64_t)g * k_s1;
+  const char* const vg = it_v + (int64_t)g * v_s1;
+  __attribute__((address_space(3))) unsigned* const take =
+      reinterpret_cast<__attribute__((address_space(3))) unsigned*>(lds + C::L_FLAG + 4);
+  int rows[NB];
+  auto refill = [&](auto slc) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slc)::value;
+    lds_t* const slot = ring + SL * C::SLOTB;
+    unsigned t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(take, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
     rsrc_t kr = none, vr = none;
-    if (rk < n_v) {
-      kr = make_rsrc(rkp, rkb);
-      vr = make_rsrc(rvp, rvb);
-      rkp += kstep;
-      rvp += vstep;
-      rkb -= (unsigned)kstep;
-      rvb -= (unsigned)vstep;
+    rows[SL] = -1;
+    if (t < nsub) {
+      const int r0 = a + kDecodeSub * (int)t;
+      const int nr = min(kDecodeSub, b - r0);
+      kr = make_rsrc(kg + (int64_t)r0 * ks2, (unsigned)((nr - 1) * ks2 + C::RB));
+      vr = make_rsrc(vg + (int64_t)r0 * vs2, (unsigned)((nr - 1) * vs2 + C::RB));
+      rows[SL] = r0;
     }
-    ++rk;
 #pragma unroll
     for (int i = 0; i < C::NDK; ++i) dma16(kr, slot + 1024 * i, offk[i]);
 #pragma unroll
     for (int i = 0; i < C::NDK; ++i) dma16(vr, slot + C::SUBB + 1024 * i, offv[i]);
   };
-#pragma unroll
-  for (int s = 0; s < NB; ++s) refill(ring + s * C::SLOTB);
+  static_for<0, NB>([&](auto slc) { refill(slc); });
   // The queries were requested first; they are in registers once at most the
   // ring's loads are outstanding (the empty asm makes the compiler wait here).
 #pragma unroll
@@ -381,9 +393,10 @@ void decode_kernel(const DecodeParams p) {
       for (int jj = 0; jj < 4; ++jj) acc[h][e][jj] = 0.f;
   }
 
-  // One sub-tile in ring slot SL (row0: its first position within the group).
-  auto process = [&](auto slc, int row0) __attribute__((always_inline)) {
+  // The sub-tile in ring slot SL.
+  auto process = [&](auto slc) __attribute__((always_inline)) {
     constexpr int SL = decltype(slc)::value;
+    const int row0 = rows[SL];
     constexpr int SOFF = SL * C::SLOTB;
     wait_vmem<C::WAIT_K>();
 
@@ -423,7 +436,7 @@ void decode_kernel(const DecodeParams p) {
     });
 
     // Online softmax (base 2); the running max is uniform over a row.
-    const bool valid = row0 + col < n_kv;
+    const bool valid = row0 + col < b;
     float pr[HS];
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
@@ -469,38 +482,22 @@ void decode_kernel(const DecodeParams p) {
       }
     wave_lds_fence();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot reads done before it is refilled
-    refill(ring + SOFF);
+    refill(slc);
   };
 
-  // Ring slots are used in turn; each case falls through to the next slot.
-  int row0 = row_first;
-  for (int k = 0; k < n_v;) {
-    switch (k & (NB - 1)) {
-      case 0:
-        process(std::integral_constant<int, 0>{}, row0);
-        row0 += NWV * kDecodeSub;
-        if (++k >= n_v) break;
-        [[fallthrough]];
-      case 1:
-        process(std::integral_constant<int, 1>{}, row0);
-        row0 += NWV * kDecodeSub;
-        if (++k >= n_v) break;
-        if constexpr (NB == 2) break;
-        [[fallthrough]];
-      case 2:
-        if constexpr (NB > 2) {
-          process(std::integral_constant<int, (NB > 2 ? 2 : 0)>{}, row0);
-          row0 += NWV * kDecodeSub;
-          if (++k >= n_v) break;
+  // Ring slots are used in turn until the first slot without a sub-tile (a
+  // wave's takes increase, so every later slot is empty too).
+  if (rows[0] >= 0) {
+    for (;;) {
+      bool done = false;
+      static_for<0, NB>([&](auto slc) {
+        constexpr int SL = decltype(slc)::value;
+        if (!done) {
+          process(slc);
+          done = rows[(SL + 1) % NB] < 0;
         }
-        [[fallthrough]];
-      default:
-        if constexpr (NB > 3) {
-          process(std::integral_constant<int, (NB > 3 ? 3 : 0)>{}, row0);
-          row0 += NWV * kDecodeSub;
-          ++k;
-        }
-        break;
+      });
+      if (done) break;
     }
   }
 
