@@ -51,34 +51,22 @@ def causal_flops(n, h, d):
     return 4 * d * h * n * (n + 1) // 2
 
 
-class Timer:
-    """Per-launch HIP events on the stream the kernels run on."""
-
-    def __init__(self, torch, n):
-        self.torch = torch
-        self.ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                   for _ in range(n)]
-
-    def mean_ms(self):
-        return sum(a.elapsed_time(b) for a, b in self.ev) / len(self.ev)
-
-
 def run_timed(torch, launch, steps, warmup):
-    """warmup untimed steps, then `steps` timed steps bracketed by synchronize;
-    returns (ms per step over the region, mean per-launch event ms)."""
+    """warmup untimed steps, then `steps` timed steps back to back, bracketed by
+    synchronize and by two HIP events on the stream the kernels run on; returns
+    ms per step. (Events between the launches would put their own commands
+    between the kernels, so the per-launch time of a one-launch step is this
+    same figure; rocprofv3 gives the kernel's own duration.)"""
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
-    t = Timer(torch, steps)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
-        t.ev[i][0].record()
         launch(i)
-        t.ev[i][1].record()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, t.mean_ms()
+    return start.elapsed_time(end) / steps
 
 
 def bench_decode(torch, mh, lib, stream, steps, warmup, n_layers=24, n_kv=4096, h=14, hkv=2,
@@ -106,7 +94,8 @@ def bench_decode(torch, mh, lib, stream, steps, warmup, n_layers=24, n_kv=4096, 
         if rc:
             raise mh.MiHipError(rc, lib.last_error())
 
-    ms, kern_ms = run_timed(torch, launch, steps, warmup)
+    ms = run_timed(torch, launch, steps, warmup)
+    kern_ms = ms  # one launch per step
     nbytes = decode_bytes(n_layers, n_kv, h, hkv, d, elt)
     return dict(ms_per_step=ms, kernel_ms=kern_ms, bytes=nbytes, sets=sets,
                 gbps=nbytes / (ms * 1e-3) / 1e9, kernel_gbps=nbytes / (kern_ms * 1e-3) / 1e9)
@@ -133,7 +122,7 @@ def bench_decode_per_layer(torch, mh, lib, stream, steps, warmup, n_layers=24, n
             if rc:
                 raise mh.MiHipError(rc, lib.last_error())
 
-    ms, _ = run_timed(torch, launch, max(5, steps // 4), max(2, warmup // 4))
+    ms = run_timed(torch, launch, max(5, steps // 4), max(2, warmup // 4))
     nbytes = decode_bytes(n_layers, n_kv, h, hkv, d, 4)
     return dict(us_per_layer=ms * 1e3 / n_layers, gbps=nbytes / (ms * 1e-3) / 1e9)
 
@@ -151,7 +140,8 @@ def bench_prefill(torch, mh, lib, stream, steps, warmup, n, h=14, hkv=2, d=64):
         if rc:
             raise mh.MiHipError(rc, lib.last_error())
 
-    ms, kern_ms = run_timed(torch, launch, steps, warmup)
+    ms = run_timed(torch, launch, steps, warmup)
+    kern_ms = ms  # one launch per step
     flops = causal_flops(n, h, d)
     return dict(n=n, ms_per_step=ms, kernel_ms=kern_ms, flops=flops,
                 tflops=flops / (kern_ms * 1e-3) / 1e12)
@@ -162,13 +152,15 @@ def bench_copy(torch, steps, warmup, nbytes=256 << 20):
     the FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = nbytes)."""
     src = torch.empty(nbytes // 4, device="cuda").uniform_()
     dst = torch.empty_like(src)
-    ms, kern_ms = run_timed(torch, lambda i: dst.copy_(src), steps, warmup)
+    kern_ms = run_timed(torch, lambda i: dst.copy_(src), steps, warmup)
     return dict(bytes=nbytes, kernel_ms=kern_ms, gbps=2 * nbytes / (kern_ms * 1e-3) / 1e9)
 
 
-def cpu_baseline(n_layers_sample=24, n_kv=4096):
-    """The reference three-node CPU path on the host cores (bounded sample:
-    24 layers' decode attention at n_kv = 4096, 1 warmup + 7 timed passes)."""
+def cpu_baseline(n_layers_sample=24, n_kv=4096, target_s=12.0):
+    """The reference three-node CPU path on the host cores, on a bounded sample
+    of the decode workload: 24 layers' decode attention at n_kv = 4096, passes
+    repeated until about `target_s` seconds of CPU work (median pass), then
+    prefill-1024 a few times."""
     import numpy as np
     from oracle import cpu_attention
     impl = cpu_attention.reference() or cpu_attention.oracle()
@@ -177,18 +169,20 @@ def cpu_baseline(n_layers_sample=24, n_kv=4096):
     qs = [rng.standard_normal((1, 14, 64), dtype=np.float32) for _ in range(n_layers_sample)]
     ks = [rng.standard_normal((n_kv, 2, 64), dtype=np.float32) for _ in range(n_layers_sample)]
     vs = [rng.standard_normal((n_kv, 2, 64), dtype=np.float32) for _ in range(n_layers_sample)]
-    t, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, threads, warmup=1, reps=7)
+    t0, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, threads, warmup=1, reps=3)
+    reps = int(min(5000, max(7, target_s / max(t0, 1e-6))))
+    t, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, threads, warmup=0, reps=reps)
     nbytes = decode_bytes(n_layers_sample, n_kv, 14, 2, 64, 4)
-    # prefill-1024 on the CPU, one timed pass (the reference computes every
-    # key, masked or not; the FLOP count below is still the causal one)
+    # prefill-1024 on the CPU (the reference computes every key, masked or
+    # not; the FLOP count below is still the causal one)
     q = rng.standard_normal((1024, 14, 64), dtype=np.float32)
     k = rng.standard_normal((1024, 2, 64), dtype=np.float32)
     v = rng.standard_normal((1024, 2, 64), dtype=np.float32)
-    tp, _ = impl.time_attention([q], [k], [v], 0, 0.125, threads, warmup=0, reps=1)
+    tp, _ = impl.time_attention([q], [k], [v], 0, 0.125, threads, warmup=1, reps=5)
     return dict(value=nbytes / t / 1e9, unit="GB/s", cores=threads, kind=impl.kind,
-                sample="24 layers x decode n_kv=4096 (14 Q / 2 KV heads, head_dim 64, F32), "
-                       "median of 7 passes after 1 warmup; attn_qk -> softmax -> attn_kqv, "
-                       "barrier per node, static (head,row) split",
+                sample=f"24 layers x decode n_kv=4096 (14 Q / 2 KV heads, head_dim 64, F32), "
+                       f"median of {reps} passes ({reps * t:.1f} s); attn_qk -> softmax -> "
+                       f"attn_kqv, barrier per node, static (head,row) split",
                 us_per_layer=t * 1e6 / n_layers_sample,
                 prefill1024_s=tp, prefill1024_tflops=causal_flops(1024, 14, 64) / tp / 1e12,
                 cpu=_cpu_model())
