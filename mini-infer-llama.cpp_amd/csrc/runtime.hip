@@ -351,6 +351,12 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
 }
 
 int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream) {
+  // a KV head's rows, up to the last key tile's end, are addressed with 32-bit
+  // byte offsets
+  const int64_t rows = (int64_t)a->n_past + a->n_tokens + mi::kPrefillKeys;
+  const int64_t row_bytes = (int64_t)r.head_dim * (r.f16 ? 2 : 4);
+  if (rows * r.k_s2 + row_bytes > INT32_MAX || rows * r.v_s2 + row_bytes > INT32_MAX)
+    return fail(MI_HIP_E_UNSUPPORTED, "n_kv * position stride exceeds 2^31 bytes for one KV head");
   mi::PrefillParams p{};
   p.k = r.k;
   p.v = r.v;
