@@ -19,7 +19,8 @@
 //      queries, pre-scaled by scale*log2(e) and held in registers;
 //   3. causal mask (key > n_past + query) on tiles that reach the diagonal,
 //      online softmax in base 2: a lane holds 16 keys of query c and its
-//      partner lane (lane ^ 32) the other 16;
+//      partner lane (lane ^ 32) the other 16 (one permlane32 swap combines
+//      them); O is rescaled only in units where a running max moved;
 //   4. O^T += V^T . P^T with 16 MFMAs per 32 output dims; S^T leaves step 3 in
 //      the B-operand layout of this product (register r of a lane = key
 //      8(r/4) + 4kh + r%4), so P needs no shuffle.
@@ -47,29 +48,54 @@ __device__ inline rsrc_t prefill_rsrc(const void* p, unsigned bytes) {
 
 template <typename KT>
 struct Elt;
+// Loads at byte offset vo (per lane) + so (wave-uniform, a scalar register);
+// only vo (with the instruction's constant offset) is range-checked.
 template <>
 struct Elt<float> {
-  // 4 consecutive elements at byte offset o
-  __device__ static void load4(rsrc_t r, unsigned o, float* d) {
-    const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+  // 4 consecutive elements
+  __device__ static void load4(rsrc_t r, unsigned vo, unsigned so, float* d) {
+    const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
     d[0] = x[0]; d[1] = x[1]; d[2] = x[2]; d[3] = x[3];
   }
-  __device__ static float load1(rsrc_t r, unsigned o) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, o, 0, 0));
+  __device__ static float load1(rsrc_t r, unsigned vo, unsigned so) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
   }
 };
 template <>
 struct Elt<_Float16> {
-  // 8 consecutive elements at byte offset o, widened exactly
-  __device__ static void load8(rsrc_t r, unsigned o, float* d) {
-    const f16x8 x = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+  // 8 consecutive elements, widened exactly
+  __device__ static void load8(rsrc_t r, unsigned vo, unsigned so, float* d) {
+    const f16x8 x = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
 #pragma unroll
     for (int i = 0; i < 8; ++i) d[i] = (float)x[i];
   }
-  __device__ static float load1(rsrc_t r, unsigned o) {
-    return (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, o, 0, 0));
+  __device__ static float load1(rsrc_t r, unsigned vo, unsigned so) {
+    return (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
   }
 };
+
+// x and lane ^ 32's x, in some order, in one v_permlane32_swap (no LDS round
+// trip): swapping the upper half of one copy of x with the lower half of
+// another leaves each lane holding both. Written as asm: the compiler's
+// builtin for this instruction drops one of its two results when they are
+// used as floats. The s_nop gives the two wait states a VALU write of an
+// operand needs before the swap reads it.
+__device__ inline void xor32_pair(float x, float& a, float& b) {
+  float y = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  a = x;
+  b = y;
+}
+__device__ inline float xor32_max(float x) {
+  float a, b;
+  xor32_pair(x, a, b);
+  return fmaxf(a, b);
+}
+__device__ inline float xor32_sum(float x) {
+  float a, b;
+  xor32_pair(x, a, b);
+  return a + b;
+}
 
 }  // namespace
 
@@ -114,24 +140,43 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   const rsrc_t vr = prefill_rsrc(p.v + (int64_t)g * p.v_s1, (unsigned)((int64_t)(n_kv - 1) * p.v_s2 + D * ELT));
   const int ks2 = (int)p.k_s2, vs2 = (int)p.v_s2;
 
-  // K and V of key tile kt in this lane's operand layouts (rows past n_kv are zero).
+  // K and V of key tile kt in this lane's operand layouts. The buffer range
+  // check covers the per-lane offset (and the instruction's constant), not the
+  // scalar one: a tile wholly below n_kv moves its wave-uniform row offsets to
+  // the scalar operand; the tile that crosses n_kv keeps the whole offset per
+  // lane, so its rows past n_kv read as zero.
+  const unsigned kvo = (unsigned)(col * ks2 + kh * HALF * ELT);
+  const unsigned vvo = (unsigned)(4 * kh * vs2 + col * ELT);
   auto load_k = [&](int kt, float (&kk)[HALF]) __attribute__((always_inline)) {
-    const unsigned ko = (unsigned)((kt * kPrefillKeys + col) * ks2 + kh * HALF * ELT);
+    const int key0 = kt * kPrefillKeys;
+    const bool whole = key0 + kPrefillKeys <= n_kv;
+    const unsigned so = whole ? (unsigned)(key0 * ks2) : 0u;
+    const unsigned vo = whole ? kvo : kvo + (unsigned)(key0 * ks2);
     if constexpr (ELT == 4) {
 #pragma unroll
-      for (int s = 0; s < HALF; s += 4) Elt<float>::load4(kr, ko + 4 * s, kk + s);
+      for (int s = 0; s < HALF; s += 4) Elt<float>::load4(kr, vo + 4 * s, so, kk + s);
     } else {
 #pragma unroll
-      for (int s = 0; s < HALF; s += 8) Elt<_Float16>::load8(kr, ko + 2 * s, kk + s);
+      for (int s = 0; s < HALF; s += 8) Elt<_Float16>::load8(kr, vo + 2 * s, so, kk + s);
     }
   };
   auto load_v = [&](int kt, float (&vv)[NV]) __attribute__((always_inline)) {
+    const int key0 = kt * kPrefillKeys;
+    if (key0 + kPrefillKeys <= n_kv) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const unsigned vo =
-          (unsigned)((kt * kPrefillKeys + 8 * (t >> 2) + 4 * kh + (t & 3)) * vs2 + col * ELT);
+      for (int t = 0; t < 16; ++t) {
+        const unsigned so = (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) vv[t * NDB + db] = Elt<KT>::load1(vr, vo + 32 * db * ELT);
+        for (int db = 0; db < NDB; ++db)
+          vv[t * NDB + db] = Elt<KT>::load1(vr, vvo + 32 * db * ELT, so);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const unsigned vo = vvo + (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) vv[t * NDB + db] = Elt<KT>::load1(vr, vo + 32 * db * ELT, 0u);
+      }
     }
   };
   auto unit_tile = [&](int u) { return u < tA ? u : u - tA; };
@@ -143,7 +188,7 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
 
   auto write_record = [&](int slot) __attribute__((always_inline)) {
     float* rec = lds + (wave * 2 + slot) * C::RECF;
-    const float ltot = lsum + __shfl_xor(lsum, 32, kWave);
+    const float ltot = xor32_sum(lsum);
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -163,13 +208,15 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
                                                      (int64_t)(qvalid ? qloc : 0) * p.q_s2 +
                                                      (int64_t)h * p.q_s1) +
                       kh * HALF;
+    // queries past n_tokens read row 0 (any finite row) and weigh zero
+    const float sc = qvalid ? p.scale_log2e : 0.f;
 #pragma unroll
     for (int s = 0; s < HALF; s += 4) {
       const float4 v = *reinterpret_cast<const float4*>(qp + s);
-      qb[s + 0] = qvalid ? v.x * p.scale_log2e : 0.f;
-      qb[s + 1] = qvalid ? v.y * p.scale_log2e : 0.f;
-      qb[s + 2] = qvalid ? v.z * p.scale_log2e : 0.f;
-      qb[s + 3] = qvalid ? v.w * p.scale_log2e : 0.f;
+      qb[s + 0] = v.x * sc;
+      qb[s + 1] = v.y * sc;
+      qb[s + 2] = v.z * sc;
+      qb[s + 3] = v.w * sc;
     }
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] = (floatx16)(0.f);
@@ -178,8 +225,8 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     cur = X;
   };
 
-  // Unit u with its K in kk; requests its V and the next unit's K (into kn)
-  // before the matrix-core work that hides them.
+  // Unit u with its K in kk: requests its V and the next unit's K (into kn)
+  // before the QK products that hide them.
   auto step = [&](int u, const float (&kk)[HALF], float (&kn)[HALF]) __attribute__((always_inline)) {
     const int X = u < tA ? qa : qz;
     const int kt = u < tA ? u : u - tA;
@@ -200,16 +247,15 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     const int key0 = kt * kPrefillKeys;
     const int qabs = p.n_past + X * kPrefillRows + col;
     const bool diag = key0 + kPrefillKeys - 1 > p.n_past + X * kPrefillRows;
-    float mx = -INFINITY;
+    if (diag) {
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      float x = s[rr];
-      if (diag && key0 + 8 * (rr >> 2) + 4 * kh + (rr & 3) > qabs) x = -INFINITY;
-      s[rr] = x;
-      mx = fmaxf(mx, x);
+      for (int rr = 0; rr < 16; ++rr)
+        if (key0 + 8 * (rr >> 2) + 4 * kh + (rr & 3) > qabs) s[rr] = -INFINITY;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float mn = fmaxf(m, mx);
+    float mx = s[0];
+#pragma unroll
+    for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, s[rr]);
+    const float mn = fmaxf(m, xor32_max(mx));
     const float mu = mn == -INFINITY ? 0.f : mn;
     const float alpha = fast_exp2(m - mu);
     float ps = 0.f;
@@ -220,9 +266,13 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       ps += e;
     }
     lsum = lsum * alpha + ps;
-    m = mn;
+    // O is rescaled only when some query's running max moved (alpha == 1 for
+    // the others, exactly).
+    if (__builtin_amdgcn_ballot_w64(mn != m)) {
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+      for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+    }
+    m = mn;
 
     // O^T += V^T . P^T
 #pragma unroll

@@ -137,6 +137,25 @@ def test_prefill_vs_oracle(hip, stream, oracle, n_past, n_tok, d, h, hkv):
     assert_close(got, ref_out(oracle, q, k, v, n_past, scale), TOL_F32)
 
 
+@pytest.mark.parametrize("n_past,n_tok,d,f16", [
+    (0, 45, 64, False), (37, 100, 64, False), (5, 200, 128, False), (11, 70, 128, True),
+    (70, 1, 64, False), (99, 1, 128, True),
+])
+def test_cache_rows_past_n_kv_are_never_used(hip, stream, oracle, n_past, n_tok, d, f16):
+    # The cache holds more rows than n_kv = n_past + n_tok and those rows are
+    # NaN: a kernel that read them into a sum (even with weight 0) would
+    # return NaN. The last key tile crosses n_kv in every case.
+    print("rows past n_kv", n_past, n_tok, d, f16, flush=True)
+    n_kv = n_past + n_tok
+    q, k, v = cpu_attention.make_inputs(31 * n_kv + d, d, 14, 2, n_kv + 40, n_tok)
+    k[n_kv:] = np.nan
+    v[n_kv:] = np.nan
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_past, scale, f16)
+    want = ref_out(oracle, q, k[:n_kv], v[:n_kv], n_past, scale, f16)
+    assert_close(got, want, TOL_F32, f"n_past={n_past} n_tok={n_tok} d={d} f16={f16}")
+
+
 def test_prefill_f16_cache(hip, stream, oracle):
     q, k, v = cpu_attention.make_inputs(4242, 64, 14, 2, 300, 257)
     got = fused(hip, stream, q, k, v, 43, 0.125, f16=True)
