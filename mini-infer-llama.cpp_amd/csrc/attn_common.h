@@ -73,6 +73,36 @@ struct PrefillParams {
 // ---------------------------------------------------------------------------
 // Device helpers.
 // ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) char lds_t;
+
+// Raw (unswizzled, stride 0) buffer descriptor word 3 of the gfx9 family.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// Descriptor over [p, p + bytes): accesses whose per-lane offset (plus the
+// instruction's constant offset) reaches bytes read zero and make no memory
+// request. The scalar offset operand is not part of that range check.
+__device__ inline rsrc_t make_rsrc(const void* p, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
+                                           kRawBufferWord3);
+}
+
+// Waits until at most N vector memory operations of this wave are in flight
+// (they complete in issue order). Needed after buffer_load ... lds, which the
+// compiler does not track.
+template <int N>
+__device__ inline void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// LDS rows of NSLOT 16-byte slots: logical slot j of row r is stored at
+// physical slot j ^ swz(r), so 16 lanes reading one slot of 16 consecutive
+// rows hit distinct banks.
+template <int NSLOT>
+__host__ __device__ constexpr int swz(int r) {
+  return NSLOT >= 16 ? (r & 15) : ((r >> 1) & (NSLOT - 1));
+}
+
 __device__ inline float wave_max(float x) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off, kWave));

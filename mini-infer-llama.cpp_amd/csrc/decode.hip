@@ -49,7 +49,6 @@
 
 namespace mi {
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
@@ -59,20 +58,6 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kSc1 = 16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-// Raw (unswizzled, stride 0) buffer descriptor word 3 of the gfx9 family.
-constexpr int kRawBufferWord3 = 0x00020000;
-
-// Descriptor over [p, p + bytes): 16-byte accesses at offsets >= bytes read
-// zero and make no memory request.
-__device__ inline rsrc_t make_rsrc(const void* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
-                                           kRawBufferWord3);
-}
-
-template <int N>
-__device__ inline void wait_vmem() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
 __device__ inline void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int I, int N, typename F>
@@ -83,12 +68,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Physical 16-byte slot of logical slot j in row r is j ^ swz(r).
-template <int NSLOT>
-__host__ __device__ constexpr int swz(int r) {
-  return NSLOT >= 16 ? (r & 15) : ((r >> 1) & (NSLOT - 1));
-}
-
 __device__ inline float row_sum16(float x) {
   x += dpp_mov<0xB1>(x);
   x += dpp_mov<0x4E>(x);
@@ -97,7 +76,6 @@ __device__ inline float row_sum16(float x) {
   return x;
 }
 
-typedef __attribute__((address_space(3))) char lds_t;
 typedef __attribute__((address_space(3))) const DecodeItem lds_item_t;
 
 // Wave-uniform copies of values read from LDS (the compiler cannot prove a

@@ -5,29 +5,37 @@
 // sees ceil((n_past + 32 (i + 1)) / 32) key tiles of 32 keys (causal). One
 // workgroup owns the query blocks i and NQ - 1 - i of one head, so every
 // workgroup has the same number of tiles (NQ + 1 + 2 n_past / 32 when the
-// blocks are full). Its NW waves cut that list of (block, tile) units into
-// equal contiguous ranges; a range crosses from block i to block NQ - 1 - i at
-// most once, where the wave parks its first block's partial result in LDS.
+// blocks are full). Its NW waves work through that list of (block, tile)
+// units: wave w starts with unit w and then takes units in order from an LDS
+// counter, so a wave that is served faster takes more; a wave's units cross
+// from block i to block NQ - 1 - i at most once, where it parks its first
+// block's partial result in LDS.
 //
 // Per unit (lane = (c = lane % 32, kh = lane / 32)):
-//   1. the tile's K rows and V columns come straight from memory (L2) into
-//      registers in the matrix-core operand layouts: lane (c, kh) holds
-//      K[key c][kh D/2 ..] and V[key][dim c + 32 db] for the 16 keys
-//      8(t/4) + 4kh + t%4; K is requested one unit ahead, V at the start of
-//      its unit, under the QK products;
-//   2. S^T = K . Q^T with D/2 v_mfma_f32_32x32x2f32: A = K, B = the block's
-//      queries, pre-scaled by scale*log2(e) and held in registers;
-//   3. causal mask (key > n_past + query) on tiles that reach the diagonal,
-//      online softmax in base 2: a lane holds 16 keys of query c and its
-//      partner lane (lane ^ 32) the other 16 (one permlane32 swap combines
-//      them); O is rescaled only in units where a running max moved;
+//   1. the key tile's 32 K rows come into the wave's LDS tile by buffer_load
+//      ... lds (no registers), four rows per instruction, 16-byte slots XOR-
+//      swizzled by row; lane (c, kh) then reads K[key c][kh D/2 ..] from it,
+//      conflict-free, as the A operand. V goes straight to registers in the
+//      A layout of the PV product (lane (c, kh) holds V[key][dim c + 32 db]
+//      for the 16 keys 8(t/4) + 4kh + t%4: one 128-byte row piece per
+//      half-wave and load);
+//   2. S^T = K . Q^T with D/2 v_mfma_f32_32x32x2f32: B = the block's queries,
+//      pre-scaled by scale*log2(e) (staged once per workgroup in LDS at
+//      head_dim 64);
+//   3. causal mask (key > n_past + query) and online softmax in base 2: a lane
+//      holds 16 keys of query c and its partner lane (lane ^ 32) the other 16
+//      (one permlane32 swap combines them);
 //   4. O^T += V^T . P^T with 16 MFMAs per 32 output dims; S^T leaves step 3 in
 //      the B-operand layout of this product (register r of a lane = key
 //      8(r/4) + 4kh + r%4), so P needs no shuffle.
-// At the end the waves' (m, l, O) records meet in LDS and each block's
-// output is merged with the stable rescaling; nothing else leaves the
-// workgroup. Two waves per SIMD at head_dim 64 (one at 128) let one wave's
-// softmax and loads run under the other's matrix-core work.
+// The units are software-pipelined: while unit u's softmax runs on the vector
+// ALUs, the next unit's QK products run on the matrix cores; the K tile after
+// that is requested as soon as the LDS tile has been read, V after the PV
+// products that consumed the previous one.
+// At the end the waves' (m, l, O) records meet in LDS and each block's output
+// is merged with the stable rescaling; nothing else leaves the workgroup. Two
+// waves per SIMD at head_dim 64 (one at 128) let one wave's vector work run
+// under the other's matrix-core work.
 #include "attn_common.h"
 #include "kernels.h"
 
@@ -36,43 +44,31 @@ namespace mi {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
+typedef __attribute__((address_space(3))) f16x8 lds_f16x8;
+typedef __attribute__((address_space(3))) float lds_f32;
+typedef __attribute__((address_space(3))) unsigned lds_u32;
 
 namespace {
 
-// Descriptor over [p, p + bytes) (raw, unswizzled): loads at offsets >= bytes
-// return zero.
-__device__ inline rsrc_t prefill_rsrc(const void* p, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+// One element at byte offset vo (per lane, range-checked) + so (wave-uniform).
+template <typename KT>
+__device__ inline float load1(rsrc_t r, unsigned vo, unsigned so);
+template <>
+__device__ inline float load1<float>(rsrc_t r, unsigned vo, unsigned so) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+}
+template <>
+__device__ inline float load1<_Float16>(rsrc_t r, unsigned vo, unsigned so) {
+  return (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
 }
 
-template <typename KT>
-struct Elt;
-// Loads at byte offset vo (per lane) + so (wave-uniform, a scalar register);
-// only vo (with the instruction's constant offset) is range-checked.
-template <>
-struct Elt<float> {
-  // 4 consecutive elements
-  __device__ static void load4(rsrc_t r, unsigned vo, unsigned so, float* d) {
-    const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
-    d[0] = x[0]; d[1] = x[1]; d[2] = x[2]; d[3] = x[3];
-  }
-  __device__ static float load1(rsrc_t r, unsigned vo, unsigned so) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
-  }
-};
-template <>
-struct Elt<_Float16> {
-  // 8 consecutive elements, widened exactly
-  __device__ static void load8(rsrc_t r, unsigned vo, unsigned so, float* d) {
-    const f16x8 x = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) d[i] = (float)x[i];
-  }
-  __device__ static float load1(rsrc_t r, unsigned vo, unsigned so) {
-    return (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
-  }
-};
+// 16 bytes per lane from r at vo (per lane, range-checked) + so (wave-uniform)
+// into LDS at lds + 16 * lane. (A plain function: in the kernel template the
+// host pass rejects the builtin's LDS pointer and drops the kernel silently.)
+__device__ inline void dma16(rsrc_t r, lds_t* lds, unsigned vo, unsigned so) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, vo, so, 0, 0);
+}
 
 // x and lane ^ 32's x, in some order, in one v_permlane32_swap (no LDS round
 // trip): swapping the upper half of one copy of x with the lower half of
@@ -82,7 +78,7 @@ struct Elt<_Float16> {
 // operand needs before the swap reads it.
 __device__ inline void xor32_pair(float x, float& a, float& b) {
   float y = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(y));
   a = x;
   b = y;
 }
@@ -102,12 +98,32 @@ __device__ inline float xor32_sum(float x) {
 template <int D, typename KT, int NW>
 struct PrefillCfg {
   static constexpr int ELT = (int)sizeof(KT);
-  static constexpr int HALF = D / 2;                        // QK MFMA steps
-  static constexpr int NDB = D / 32;                        // PV output blocks of 32 dims
-  static constexpr int NV = 16 * NDB;                       // V values per lane per tile
-  static constexpr int RS = D + 4;                          // record row stride (floats)
+  static constexpr int HALF = D / 2;                   // QK MFMA steps
+  static constexpr int NDB = D / 32;                   // PV output blocks of 32 dims
+  static constexpr int NV = 16 * NDB;                  // V values per lane per tile
+  static constexpr int RB = D * ELT;                   // bytes per K row
+  static constexpr int NSLOT = RB / 16;                // 16-byte slots per K row
+  static constexpr int KTILE = kPrefillKeys * RB;      // bytes of one K tile
+  static constexpr int NDK = KTILE / 1024;             // 1 KB loads per K tile
+  static constexpr int HSL = HALF * ELT / 16;          // slots per half row
+  static constexpr int RS = D + 4;                     // record row stride (floats)
   static constexpr int RECF = kPrefillRows * RS + 2 * kPrefillRows;  // O rows, m, l
-  static constexpr int LDS = NW * 2 * RECF * 4;             // a record per (wave, block)
+  static constexpr int RECB = RECF * 4;
+  static constexpr int REG = (KTILE > RECB ? KTILE : RECB);  // K tile, later block-qz record
+  static constexpr bool QLDS = D == 64;                // queries staged in LDS
+  static constexpr int QRS = D + 4;                    // staged query row stride (floats)
+  // LDS layout (bytes): block-qa records, per-wave K tile / block-qz record,
+  // staged queries, unit counter
+  static constexpr int L_REC0 = 0;
+  static constexpr int L_REG = L_REC0 + NW * RECB;
+  static constexpr int L_Q = L_REG + NW * REG;
+  static constexpr int L_CTR = L_Q + (QLDS ? 2 * kPrefillRows * QRS * 4 : 0);
+  static constexpr int LDS = L_CTR + 16;
+  // vector memory operations a wave issues after a K tile request and before
+  // the next tile's wait (the V loads of one unit), capped at the counter's range
+  static constexpr int WAIT_K = NV < 63 ? NV : 63;
+  static_assert(KTILE % 1024 == 0, "1 KB load granularity");
+  static_assert(REG % 16 == 0 && RECB % 16 == 0, "16-byte alignment");
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
@@ -115,8 +131,10 @@ template <int D, typename KT, int NW>
 __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams p) {
   typedef PrefillCfg<D, KT, NW> C;
   constexpr int HALF = C::HALF, NDB = C::NDB, NV = C::NV, RS = C::RS, ELT = C::ELT;
+  constexpr int NSLOT = C::NSLOT;
 
-  extern __shared__ __attribute__((aligned(16))) float lds[];
+  extern __shared__ __attribute__((aligned(16))) char lds_raw[];
+  lds_t* const lds = (lds_t*)lds_raw;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int col = lane & 31;
@@ -132,92 +150,133 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   };
   const int tA = tiles(qa);
   const int T = tA + (qz != qa ? tiles(qz) : 0);
-  auto first_unit = [&](int w) { return T * w / NW; };
-  const int u0 = first_unit(wave), u1 = first_unit(wave + 1);
+  auto blk = [&](int u) { return u < tA ? qa : qz; };
+  auto unit_tile = [&](int u) { return u < tA ? u : u - tA; };
 
   const int g = h / p.n_rep;
-  const rsrc_t kr = prefill_rsrc(p.k + (int64_t)g * p.k_s1, (unsigned)((int64_t)(n_kv - 1) * p.k_s2 + D * ELT));
-  const rsrc_t vr = prefill_rsrc(p.v + (int64_t)g * p.v_s1, (unsigned)((int64_t)(n_kv - 1) * p.v_s2 + D * ELT));
+  const rsrc_t kr = make_rsrc(p.k + (int64_t)g * p.k_s1, (unsigned)((int64_t)(n_kv - 1) * p.k_s2 + D * ELT));
+  const rsrc_t vr = make_rsrc(p.v + (int64_t)g * p.v_s1, (unsigned)((int64_t)(n_kv - 1) * p.v_s2 + D * ELT));
   const int ks2 = (int)p.k_s2, vs2 = (int)p.v_s2;
 
-  // K and V of key tile kt in this lane's operand layouts. The buffer range
-  // check covers the per-lane offset (and the instruction's constant), not the
-  // scalar one: a tile wholly below n_kv moves its wave-uniform row offsets to
-  // the scalar operand; the tile that crosses n_kv keeps the whole offset per
-  // lane, so its rows past n_kv read as zero.
-  const unsigned kvo = (unsigned)(col * ks2 + kh * HALF * ELT);
-  const unsigned vvo = (unsigned)(4 * kh * vs2 + col * ELT);
-  auto load_k = [&](int kt, float (&kk)[HALF]) __attribute__((always_inline)) {
+  // K tile of key tile kt into this wave's LDS tile: load i fills bytes
+  // [1024 i, +1024), lane L its 16 bytes at 1024 i + 16 L, i.e. physical slot
+  // pj of row r, which holds logical slot pj ^ swz(r). A tile wholly below
+  // n_kv passes its row offset as the (unchecked) scalar offset; the tile that
+  // crosses n_kv keeps it in the range-checked per-lane offset, so its rows
+  // past n_kv arrive as zeros.
+  lds_t* const ktile = lds + C::L_REG + wave * C::REG;
+  unsigned koff[C::NDK];
+#pragma unroll
+  for (int i = 0; i < C::NDK; ++i) {
+    const int o = 1024 * i + 16 * lane;
+    const int r = o / C::RB;
+    koff[i] = (unsigned)(r * ks2 + 16 * (((o % C::RB) / 16) ^ swz<NSLOT>(r)));
+  }
+  auto request_k = [&](int kt) __attribute__((always_inline)) {
     const int key0 = kt * kPrefillKeys;
-    const bool whole = key0 + kPrefillKeys <= n_kv;
-    const unsigned so = whole ? (unsigned)(key0 * ks2) : 0u;
-    const unsigned vo = whole ? kvo : kvo + (unsigned)(key0 * ks2);
-    if constexpr (ELT == 4) {
+    const unsigned to_lane = key0 + kPrefillKeys <= n_kv ? 0u : ~0u;
+    const unsigned row = (unsigned)(key0 * ks2);
 #pragma unroll
-      for (int s = 0; s < HALF; s += 4) Elt<float>::load4(kr, vo + 4 * s, so, kk + s);
-    } else {
+    for (int i = 0; i < C::NDK; ++i)
+      dma16(kr, ktile + 1024 * i, koff[i] + (row & to_lane), row & ~to_lane);
+  };
+  // A operand of QK: K[key c][kh D/2 + s], s < D/2, from the LDS tile.
+  auto read_k = [&](float (&kk)[HALF]) __attribute__((always_inline)) {
+    const lds_t* const rowp = ktile + col * C::RB;
 #pragma unroll
-      for (int s = 0; s < HALF; s += 8) Elt<_Float16>::load8(kr, vo + 2 * s, so, kk + s);
+    for (int q = 0; q < C::HSL; ++q) {
+      const lds_t* const a = rowp + 16 * ((kh * C::HSL + q) ^ swz<NSLOT>(col));
+      if constexpr (ELT == 4) {
+        const f32x4 x = *reinterpret_cast<const lds_f32x4*>(a);
+        kk[4 * q + 0] = x[0]; kk[4 * q + 1] = x[1]; kk[4 * q + 2] = x[2]; kk[4 * q + 3] = x[3];
+      } else {
+        const f16x8 x = *reinterpret_cast<const lds_f16x8*>(a);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kk[8 * q + e] = (float)x[e];
+      }
     }
   };
+  // A operand of PV for key tile kt (rows past n_kv are zero, as for K).
+  const unsigned vvo = (unsigned)(4 * kh * vs2 + col * ELT);
   auto load_v = [&](int kt, float (&vv)[NV]) __attribute__((always_inline)) {
     const int key0 = kt * kPrefillKeys;
-    if (key0 + kPrefillKeys <= n_kv) {
+    const unsigned to_lane = key0 + kPrefillKeys <= n_kv ? 0u : ~0u;
 #pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const unsigned so = (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
+    for (int t = 0; t < 16; ++t) {
+      const unsigned row = (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
+      const unsigned vo = vvo + (row & to_lane), so = row & ~to_lane;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
-          vv[t * NDB + db] = Elt<KT>::load1(vr, vvo + 32 * db * ELT, so);
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < 16; ++t) {
-        const unsigned vo = vvo + (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) vv[t * NDB + db] = Elt<KT>::load1(vr, vo + 32 * db * ELT, 0u);
-      }
+      for (int db = 0; db < NDB; ++db) vv[t * NDB + db] = load1<KT>(vr, vo + 32 * db * ELT, so);
     }
   };
-  auto unit_tile = [&](int u) { return u < tA ? u : u - tA; };
+
+  // The first unit of each wave is fixed (unit `wave`): its K tile is
+  // requested before the workgroup's setup.
+  if (wave < T) request_k(unit_tile(wave));
+
+  // Setup: the unit counter (the next unit to take), block-qa records that are
+  // never written keep m = -inf, and at head_dim 64 the pre-scaled queries of
+  // both blocks.
+  lds_u32* const ctr = (lds_u32*)(lds + C::L_CTR);
+  auto rec_at = [&](int w, int slot) __attribute__((always_inline)) {
+    return (lds_f32*)(lds + (slot == 0 ? C::L_REC0 + w * C::RECB : C::L_REG + w * C::REG));
+  };
+  if (threadIdx.x == 0) *ctr = (unsigned)NW;
+  if (lane < kPrefillRows) rec_at(wave, 0)[kPrefillRows * RS + lane] = -INFINITY;
+  if constexpr (C::QLDS) {
+    constexpr int BQ4 = kPrefillRows * D / 4;  // float4 pieces of one block
+#pragma unroll
+    for (int i = threadIdx.x; i < 2 * BQ4; i += NW * kWave) {
+      const int b = i / BQ4, row = (i % BQ4) / (D / 4), d4 = i % (D / 4);
+      const int qloc = (b == 0 ? qa : qz) * kPrefillRows + row;
+      const bool qvalid = qloc < p.n_tokens;
+      // queries past n_tokens read row 0 (any finite row) and weigh zero
+      const float4 v = *reinterpret_cast<const float4*>(
+          reinterpret_cast<const char*>(p.q) + (int64_t)(qvalid ? qloc : 0) * p.q_s2 +
+          (int64_t)h * p.q_s1 + 16 * d4);
+      const float sc = qvalid ? p.scale_log2e : 0.f;
+      *reinterpret_cast<lds_f32x4*>(lds + C::L_Q + ((b * kPrefillRows + row) * C::QRS + 4 * d4) * 4) =
+          f32x4{v.x * sc, v.y * sc, v.z * sc, v.w * sc};
+    }
+  }
+  __syncthreads();
+  auto take = [&]() __attribute__((always_inline)) {
+    unsigned t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    return __builtin_amdgcn_readfirstlane((int)t);
+  };
 
   float qb[HALF];
   floatx16 o[NDB];
   float m = -INFINITY, lsum = 0.f;
   int cur = -1;  // query block of the running state
 
-  auto write_record = [&](int slot) __attribute__((always_inline)) {
-    float* rec = lds + (wave * 2 + slot) * C::RECF;
-    const float ltot = xor32_sum(lsum);
+  // The block's queries (pre-scaled by scale*log2(e)) into qb.
+  auto load_q = [&](int X) __attribute__((always_inline)) {
+    if constexpr (C::QLDS) {
+      const lds_t* const qp =
+          lds + C::L_Q + (((X == qa ? 0 : 1) * kPrefillRows + col) * C::QRS + kh * HALF) * 4;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+      for (int s = 0; s < HALF; s += 4) {
+        const f32x4 v = *reinterpret_cast<const lds_f32x4*>(qp + 4 * s);
+        qb[s + 0] = v[0]; qb[s + 1] = v[1]; qb[s + 2] = v[2]; qb[s + 3] = v[3];
+      }
+    } else {
+      const int qloc = X * kPrefillRows + col;
+      const bool qvalid = qloc < p.n_tokens;
+      const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.q) +
+                                                       (int64_t)(qvalid ? qloc : 0) * p.q_s2 +
+                                                       (int64_t)h * p.q_s1) +
+                        kh * HALF;
+      const float sc = qvalid ? p.scale_log2e : 0.f;
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        *reinterpret_cast<f32x4*>(rec + col * RS + 32 * db + 8 * r4 + 4 * kh) =
-            f32x4{o[db][4 * r4 + 0], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]};
-    if (kh == 0) {
-      rec[kPrefillRows * RS + col] = m;
-      rec[kPrefillRows * RS + kPrefillRows + col] = ltot;
+      for (int s = 0; s < HALF; s += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(qp + s);
+        qb[s + 0] = v.x * sc; qb[s + 1] = v.y * sc; qb[s + 2] = v.z * sc; qb[s + 3] = v.w * sc;
+      }
     }
   };
-
-  auto start_block = [&](int X) __attribute__((always_inline)) {
-    const int qloc = X * kPrefillRows + col;
-    const bool qvalid = qloc < p.n_tokens;
-    const float* qp = reinterpret_cast<const float*>(reinterpret_cast<const char*>(p.q) +
-                                                     (int64_t)(qvalid ? qloc : 0) * p.q_s2 +
-                                                     (int64_t)h * p.q_s1) +
-                      kh * HALF;
-    // queries past n_tokens read row 0 (any finite row) and weigh zero
-    const float sc = qvalid ? p.scale_log2e : 0.f;
-#pragma unroll
-    for (int s = 0; s < HALF; s += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(qp + s);
-      qb[s + 0] = v.x * sc;
-      qb[s + 1] = v.y * sc;
-      qb[s + 2] = v.z * sc;
-      qb[s + 3] = v.w * sc;
-    }
+  auto reset = [&](int X) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < NDB; ++db) o[db] = (floatx16)(0.f);
     m = -INFINITY;
@@ -225,33 +284,38 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     cur = X;
   };
 
-  // Unit u with its K in kk: requests its V and the next unit's K (into kn)
-  // before the QK products that hide them.
-  auto step = [&](int u, const float (&kk)[HALF], float (&kn)[HALF]) __attribute__((always_inline)) {
-    const int X = u < tA ? qa : qz;
-    const int kt = u < tA ? u : u - tA;
-    if (X != cur) {
-      if (cur >= 0) write_record(0);  // the first block's part of this wave's range
-      start_block(X);
+  // (m, l, O) of this wave's part of a block into its record.
+  auto write_record = [&](int slot) __attribute__((always_inline)) {
+    lds_f32* const rec = rec_at(wave, slot);
+    const float ltot = xor32_sum(lsum);
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+        *reinterpret_cast<lds_f32x4*>(rec + col * RS + 32 * db + 8 * r4 + 4 * kh) =
+            f32x4{o[db][4 * r4 + 0], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]};
+    if (kh == 0) {
+      rec[kPrefillRows * RS + col] = m;
+      rec[kPrefillRows * RS + kPrefillRows + col] = ltot;
     }
-    float vv[NV];
-    load_v(kt, vv);
-    if (u + 1 < u1) load_k(unit_tile(u + 1), kn);
+  };
 
-    // S^T = K . Q^T
+  // S^T = K . Q^T
+  auto qk = [&](const float (&kk)[HALF]) __attribute__((always_inline)) {
     floatx16 s = (floatx16)(0.f);
 #pragma unroll
     for (int st = 0; st < HALF; ++st) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[st], qb[st], s, 0, 0, 0);
+    return s;
+  };
 
-    // Causal mask and online softmax (base 2).
-    const int key0 = kt * kPrefillKeys;
-    const int qabs = p.n_past + X * kPrefillRows + col;
-    const bool diag = key0 + kPrefillKeys - 1 > p.n_past + X * kPrefillRows;
-    if (diag) {
+  // Causal mask and online softmax (base 2) of unit (block X, tile kt): s
+  // becomes the probabilities, (m, lsum, O) move on. No branches, so the
+  // compiler can interleave it with the next unit's QK products.
+  auto softmax = [&](floatx16& s, int X, int kt) __attribute__((always_inline)) {
+    const int lim = p.n_past + X * kPrefillRows + col - kt * kPrefillKeys - 4 * kh;
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr)
-        if (key0 + 8 * (rr >> 2) + 4 * kh + (rr & 3) > qabs) s[rr] = -INFINITY;
-    }
+    for (int rr = 0; rr < 16; ++rr)
+      if (8 * (rr >> 2) + (rr & 3) > lim) s[rr] = -INFINITY;
     float mx = s[0];
 #pragma unroll
     for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, s[rr]);
@@ -266,15 +330,13 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       ps += e;
     }
     lsum = lsum * alpha + ps;
-    // O is rescaled only when some query's running max moved (alpha == 1 for
-    // the others, exactly).
-    if (__builtin_amdgcn_ballot_w64(mn != m)) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-    }
+    for (int db = 0; db < NDB; ++db) o[db] *= alpha;
     m = mn;
+  };
 
-    // O^T += V^T . P^T
+  // O^T += V^T . P^T
+  auto pv = [&](const floatx16& s, const float (&vv)[NV]) __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < 16; ++t)
 #pragma unroll
@@ -282,18 +344,58 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
         o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t * NDB + db], s[t], o[db], 0, 0, 0);
   };
 
-  // The range; K alternates between two register sets.
-  float ka[HALF], kb[HALF];
-  if (u0 < u1) load_k(unit_tile(u0), ka);
-  for (int u = u0; u < u1; u += 2) {
-    step(u, ka, kb);
-    if (u + 1 >= u1) break;
-    step(u + 1, kb, ka);
+  // The wave's units, software-pipelined (see the header). Request order per
+  // iteration: the next unit's K tile, then the current V loads; the wait
+  // before reading a K tile allows the WAIT_K loads issued after it.
+  float kk[HALF], vv[NV];
+  floatx16 sc;
+  int u = wave;
+  if (u < T) {
+    load_q(blk(u));
+    reset(blk(u));
+    wait_vmem<0>();
+    read_k(kk);
+    sc = qk(kk);
+    int un = take();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile is read before it is refilled
+    if (un < T) request_k(unit_tile(un));
+    __builtin_amdgcn_sched_barrier(0);
+    load_v(unit_tile(u), vv);
+    while (un < T) {
+      // sc: scores of unit u; the LDS tile is filling with unit un's K
+      const int unn = take();
+      const int Xu = blk(u), Xn = blk(un);
+      if (Xn != Xu) load_q(Xn);  // the running state still belongs to Xu
+      wait_vmem<C::WAIT_K>();
+      read_k(kk);
+      const floatx16 sn = qk(kk);
+      softmax(sc, Xu, unit_tile(u));
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // (unconditional, the last unit's tile past the end, so the loop body
+      // has no branch around it)
+      request_k(unit_tile(min(unn, T - 1)));
+      __builtin_amdgcn_sched_barrier(0);
+      pv(sc, vv);
+      if (Xn != Xu) {
+        write_record(0);  // this wave's part of block qa
+        reset(Xn);
+      }
+      load_v(unit_tile(un), vv);
+      sc = sn;
+      u = un;
+      un = unn;
+    }
+    // the last unit: no next QK to overlap
+    softmax(sc, blk(u), unit_tile(u));
+    pv(sc, vv);
+    wait_vmem<0>();  // the last tile request lands before the region becomes a record
+    write_record(cur == qa ? 0 : 1);
   }
-  if (cur >= 0) write_record(cur == qa ? 0 : 1);
+  // a wave without a block-qz record marks its region (it held a K tile)
+  if ((cur != qz || qz == qa) && lane < kPrefillRows) rec_at(wave, 1)[kPrefillRows * RS + lane] = -INFINITY;
   __syncthreads();
 
-  // Merge: for each block, the waves whose ranges touched it.
+  // Merge: for each block, the waves that took part of it.
   constexpr int NQ4 = kPrefillRows * D / 4;  // (row, 4 dims) per block
 #pragma unroll
   for (int slot = 0; slot < 2; ++slot) {
@@ -303,21 +405,15 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       const int row = idx / (D / 4), d4 = idx % (D / 4);
       if (X * kPrefillRows + row >= p.n_tokens) continue;
       float mx = -INFINITY;
-      for (int w = 0; w < NW; ++w) {
-        const int a = first_unit(w), b = first_unit(w + 1);
-        const bool touched = slot == 0 ? a < min(b, tA) : max(a, tA) < b;
-        if (touched) mx = fmaxf(mx, lds[(w * 2 + slot) * C::RECF + kPrefillRows * RS + row]);
-      }
+      for (int w = 0; w < NW; ++w) mx = fmaxf(mx, rec_at(w, slot)[kPrefillRows * RS + row]);
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
       float l = 0.f;
       for (int w = 0; w < NW; ++w) {
-        const int a = first_unit(w), b = first_unit(w + 1);
-        const bool touched = slot == 0 ? a < min(b, tA) : max(a, tA) < b;
-        if (!touched) continue;
-        const float* rec = lds + (w * 2 + slot) * C::RECF;
+        const lds_f32* const rec = rec_at(w, slot);
         const float mw = rec[kPrefillRows * RS + row];
-        const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);
-        acc += wt * *reinterpret_cast<const f32x4*>(rec + row * RS + 4 * d4);
+        if (mw == -INFINITY) continue;  // a record the wave never wrote (any other m is finite)
+        const float wt = fast_exp2(mw - mx);
+        acc += wt * *reinterpret_cast<const lds_f32x4*>(rec + row * RS + 4 * d4);
         l += wt * rec[kPrefillRows * RS + kPrefillRows + row];
       }
       float* op = reinterpret_cast<float*>(reinterpret_cast<char*>(p.out) +

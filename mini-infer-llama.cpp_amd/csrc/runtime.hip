@@ -357,6 +357,9 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   const int64_t row_bytes = (int64_t)r.head_dim * (r.f16 ? 2 : 4);
   if (rows * r.k_s2 + row_bytes > INT32_MAX || rows * r.v_s2 + row_bytes > INT32_MAX)
     return fail(MI_HIP_E_UNSUPPORTED, "n_kv * position stride exceeds 2^31 bytes for one KV head");
+  // rows past n_kv must lie past the range the kernel's loads are bounded by
+  if (r.k_s2 < row_bytes || r.v_s2 < row_bytes)
+    return fail(MI_HIP_E_UNSUPPORTED, "K/V position stride below one row");
   mi::PrefillParams p{};
   p.k = r.k;
   p.v = r.v;
