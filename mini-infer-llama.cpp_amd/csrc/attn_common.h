@@ -45,9 +45,10 @@ struct DecodeParams {
   int32_t n_head_kv;
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
   int32_t n_wg;         // workgroups
+  int32_t cst;          // arrival counters per group: 1 + teams of its largest item
   float scale_log2e;    // softmax scale * log2(e)
   float* rec;           // one record per workgroup
-  unsigned* cnt;        // one arrival counter per (item, group); zero between launches
+  unsigned* cnt;        // cst arrival counters per (item, group); zero between launches
 };
 
 // ---------------------------------------------------------------------------

@@ -33,10 +33,13 @@
 //
 // Combining. At the end the waves' (m, l, acc) meet in LDS. With kpg == 1 the
 // workgroup writes O. Otherwise it writes one record (agent-scope atomic
-// stores, which bypass the non-coherent L2) and bumps the group's arrival
-// counter; the workgroup that arrives last reads the group's kpg records
-// (agent-scope atomic loads) and writes O with the stable rescaling
-// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s, then re-arms the counter.
+// stores, which bypass the non-coherent L2) and bumps its team's arrival
+// counter (a team: up to as many workgroups as one merge round reads); the
+// workgroup that arrives last reads the team's records (agent-scope atomic
+// loads) and merges them with the stable rescaling
+// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s. With one team it writes
+// O; otherwise the team result becomes a record again and the last team
+// merges the team records the same way. Every merger re-arms its counter.
 // Ordering without fences: each wave waits for its record stores (vmcnt 0)
 // before the workgroup barrier that precedes the counter increment, and the
 // reader issues its loads only after the increment returned. (A device-scope
@@ -536,80 +539,123 @@ void decode_kernel(const DecodeParams p) {
   wait_vmem<0>();  // no LDS DMA outlives the workgroup; record stores have completed
   if (kpg == 1) return;
 
-  // Cross-workgroup combine by the group's last arriving workgroup.
-  wg_barrier();
-  unsigned* flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
-  if (threadIdx.x == 0) {
-    const unsigned old =
-        __hip_atomic_fetch_add(p.cnt + gid, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    flag[0] = old == (unsigned)(kpg - 1) ? 1u : 0u;
-  }
-  wg_barrier();
-  if (!__builtin_amdgcn_readfirstlane(flag[0])) return;
-
+  // Cross-workgroup combine. The group's workgroups form teams of up to TEAM
+  // (as many records as one merge round below reads). The last workgroup to
+  // arrive in a team merges the team's records; with one team it writes O,
+  // otherwise it stores the result as the record of the team's first part
+  // and the last team to arrive merges the team records and writes O. Each
+  // merger re-arms the counter it completed. Counters of group gid:
+  // cnt[gid * cst] (teams), cnt[gid * cst + 1 + team].
   constexpr int NP = HSL * D / 4;             // (head slot, float4) pairs
   constexpr int NSUB = NWV * kWave / NP;      // record subsets
   static_assert(NSUB >= 1, "one pair per thread");
   constexpr int RB8 = 8;                      // records per subset requested at once
+  constexpr int TEAM = NSUB * RB8;            // records one round reads
+  const int n_teams = (kpg + TEAM - 1) / TEAM;
+  const int team = part / TEAM, team_first = team * TEAM;
+  const int team_n = min(TEAM, kpg - team_first);
+  unsigned* const gcnt = p.cnt + (int64_t)gid * p.cst;
+  unsigned* flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
+  // arrive at counter c, expecting n arrivals: true for the last one
+  auto arrive = [&](unsigned* c, int n) __attribute__((always_inline)) {
+    wg_barrier();
+    if (threadIdx.x == 0) {
+      const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      flag[0] = old == (unsigned)(n - 1) ? 1u : 0u;
+    }
+    wg_barrier();
+    return __builtin_amdgcn_readfirstlane(flag[0]) != 0;
+  };
+  if (!arrive(gcnt + 1 + team, team_n)) return;
+
   const int tt = threadIdx.x;
   const int pair = tt % NP, sub = tt / NP;
   const int hs = pair / (D / 4), cq = pair % (D / 4);
   const unsigned rec0 = (unsigned)((wg - part) * C::REC * 4);  // the group's first record (bytes)
-  float mx = -INFINITY, lt = 0.f;
-  f32x4 at = {0.f, 0.f, 0.f, 0.f};
-  if (sub < NSUB) {
-    for (int r0 = sub; r0 < kpg; r0 += RB8 * NSUB) {
-      float mr[RB8], lr[RB8];
-      f32x4 ar[RB8];
-#pragma unroll
-      for (int i = 0; i < RB8; ++i) {  // clamped indices: every load is issued, extras weigh 0
-        const unsigned rb = rec0 + (unsigned)(min(r0 + i * NSUB, kpg - 1) * C::REC * 4);
-        const f32x2 ml = __builtin_bit_cast(
-            f32x2, __builtin_amdgcn_raw_buffer_load_b64(recr, rb + 4 * (HSL * D + 2 * hs), 0, kSc1));
-        mr[i] = ml.x;
-        lr[i] = ml.y;
-        ar[i] = __builtin_bit_cast(
-            f32x4, __builtin_amdgcn_raw_buffer_load_b128(recr, rb + 4 * (hs * D + 4 * cq), 0, kSc1));
-      }
-#pragma unroll
-      for (int i = 0; i < RB8; ++i) {
-        const float mi = r0 + i * NSUB < kpg ? mr[i] : -INFINITY;
-        const float mn = fmaxf(mx, mi);
-        const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
-        const float wn = mi == -INFINITY ? 0.f : fast_exp2(mi - mn);
-        lt = lt * wo + lr[i] * wn;
-        at = at * wo + ar[i] * wn;
-        mx = mn;
-      }
-    }
-  }
-  if constexpr (NSUB > 1) {
-    float* tmp = reinterpret_cast<float*>(lds_dyn + C::L_RING);  // the ring is drained
+  // Stable merge of the records first, first + stride, ... (count of them);
+  // subset 0 ends with the result.
+  auto merge = [&](int first, int count, int stride, float& mx, float& lt, f32x4& at)
+                   __attribute__((always_inline)) {
+    mx = -INFINITY;
+    lt = 0.f;
+    at = f32x4{0.f, 0.f, 0.f, 0.f};
     if (sub < NSUB) {
-      tmp[(sub * NP + pair) * 6 + 0] = mx;
-      tmp[(sub * NP + pair) * 6 + 1] = lt;
+      for (int r0 = sub; r0 < count; r0 += RB8 * NSUB) {
+        float mr[RB8], lr[RB8];
+        f32x4 ar[RB8];
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) tmp[(sub * NP + pair) * 6 + 2 + jj] = at[jj];
-    }
-    wg_barrier();
-    if (sub == 0) {
+        for (int i = 0; i < RB8; ++i) {  // clamped indices: every load is issued, extras weigh 0
+          const unsigned rb = rec0 + (unsigned)((first + min(r0 + i * NSUB, count - 1) * stride) * C::REC * 4);
+          const f32x2 ml = __builtin_bit_cast(
+              f32x2, __builtin_amdgcn_raw_buffer_load_b64(recr, rb + 4 * (HSL * D + 2 * hs), 0, kSc1));
+          mr[i] = ml.x;
+          lr[i] = ml.y;
+          ar[i] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(recr, rb + 4 * (hs * D + 4 * cq), 0, kSc1));
+        }
 #pragma unroll
-      for (int s2 = 1; s2 < NSUB; ++s2) {
-        const float* e = tmp + (s2 * NP + pair) * 6;
-        const float mn = fmaxf(mx, e[0]);
-        const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
-        const float wn = e[0] == -INFINITY ? 0.f : fast_exp2(e[0] - mn);
-        lt = lt * wo + e[1] * wn;
-        at = at * wo + f32x4{e[2], e[3], e[4], e[5]} * wn;
-        mx = mn;
+        for (int i = 0; i < RB8; ++i) {
+          const float mi = r0 + i * NSUB < count ? mr[i] : -INFINITY;
+          const float mn = fmaxf(mx, mi);
+          const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+          const float wn = mi == -INFINITY ? 0.f : fast_exp2(mi - mn);
+          lt = lt * wo + lr[i] * wn;
+          at = at * wo + ar[i] * wn;
+          mx = mn;
+        }
       }
     }
+    if constexpr (NSUB > 1) {
+      float* tmp = reinterpret_cast<float*>(lds_dyn + C::L_RING);  // the ring is drained
+      if (sub < NSUB) {
+        tmp[(sub * NP + pair) * 6 + 0] = mx;
+        tmp[(sub * NP + pair) * 6 + 1] = lt;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) tmp[(sub * NP + pair) * 6 + 2 + jj] = at[jj];
+      }
+      wg_barrier();
+      if (sub == 0) {
+#pragma unroll
+        for (int s2 = 1; s2 < NSUB; ++s2) {
+          const float* e = tmp + (s2 * NP + pair) * 6;
+          const float mn = fmaxf(mx, e[0]);
+          const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+          const float wn = e[0] == -INFINITY ? 0.f : fast_exp2(e[0] - mn);
+          lt = lt * wo + e[1] * wn;
+          at = at * wo + f32x4{e[2], e[3], e[4], e[5]} * wn;
+          mx = mn;
+        }
+      }
+    }
+  };
+  auto write_out = [&](float lt, f32x4 at) __attribute__((always_inline)) {
+    if (sub == 0 && hs < G) {
+      float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
+      *reinterpret_cast<f32x4*>(o + 4 * cq) = at * (1.f / lt);
+    }
+  };
+
+  float mx, lt;
+  f32x4 at;
+  merge(team_first, team_n, 1, mx, lt, at);
+  if (tt == 0) __hip_atomic_store(gcnt + 1 + team, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (n_teams == 1) {
+    write_out(lt, at);
+    return;
   }
-  if (sub == 0 && hs < G) {
-    float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
-    *reinterpret_cast<f32x4*>(o + 4 * cq) = at * (1.f / lt);
+  // the team's result replaces the record of its first part (all read above)
+  if (sub == 0) {
+    const unsigned r0 = rec0 + (unsigned)(team_first * C::REC * 4);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, at), recr, r0 + 4 * (hs * D + 4 * cq), 0, kSc1);
+    if (cq == 0)
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, f32x2{mx, lt}), recr,
+                                            r0 + 4 * (HSL * D + 2 * hs), 0, kSc1);
   }
-  if (tt == 0) __hip_atomic_store(p.cnt + gid, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  wait_vmem<0>();
+  if (!arrive(gcnt, n_teams)) return;
+  merge(0, n_teams, TEAM, mx, lt, at);
+  write_out(lt, at);
+  if (tt == 0) __hip_atomic_store(gcnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Waves per workgroup: two per SIMD at head_dim 64 (a 128 KB ring still gives
@@ -638,6 +684,13 @@ static hipError_t launch_decode_h(const DecodeParams& p, int group, hipStream_t 
 }
 
 int decode_wg_waves(int head_dim) { return head_dim == 64 ? 8 : 4; }
+
+// Records one merge round reads (the team size of the cross-workgroup combine).
+int decode_team(int head_dim, int group) {
+  const int hsl = group > 4 ? 8 : 4;
+  const int threads = decode_wg_waves(head_dim) * kWave;
+  return threads / (hsl * head_dim / 4) * 8;
+}
 
 int decode_group_size(int n_rep) {
   static const int kSizes[] = {8, 7, 6, 5, 4, 3, 2, 1};

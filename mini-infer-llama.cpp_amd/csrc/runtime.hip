@@ -58,8 +58,8 @@ struct State {
   bool ready = false;
   std::atomic<uint64_t> n_malloc{0}, n_free{0}, live{0}, peak{0};
   std::atomic<uint64_t> limit{0};
-  // Shared split/merge workspace (partial records of the decode splits and
-  // of split prefill query blocks), grown on demand, never shrunk.
+  // Decode workspace (arrival counters and cross-workgroup records), grown on
+  // demand, never shrunk.
   char* ws = nullptr;
   size_t ws_bytes = 0;
   int n_cu = 0;  // compute units of the device
@@ -307,9 +307,6 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
   if (rc) return rc;
   const int elt = r0.f16 ? 2 : 4;
   const int gpi = r0.n_head_kv * (items[0].n_rep / mi::decode_group_size(items[0].n_rep));
-  if ((size_t)mi::kDecodeMaxItems * gpi * sizeof(unsigned) > kCounterBytes)
-    return fail(MI_HIP_E_UNSUPPORTED, "too many heads for one decode launch (%d groups per item)",
-                gpi);
   // Launches of up to kDecodeMaxItems consecutive items sharing the position
   // strides (the kernel's per-lane load offsets derive from them).
   int base = 0;
@@ -332,6 +329,14 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
                     "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + cnt);
     }
     const DecodePlan plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim);
+    // arrival counters: one per combine team plus one per group
+    const int team = mi::decode_team(r0.head_dim, plan.group);
+    int max_kpg = 1;
+    for (int i = 0; i < cnt; ++i) max_kpg = std::max(max_kpg, (int)p.item[i].kpg);
+    p.cst = 1 + (max_kpg + team - 1) / team;
+    if ((size_t)cnt * gpi * p.cst * sizeof(unsigned) > kCounterBytes)
+      return fail(MI_HIP_E_UNSUPPORTED, "decode launch needs %zu arrival counters (%zu available)",
+                  (size_t)cnt * gpi * p.cst, kCounterBytes / sizeof(unsigned));
     const size_t rec_bytes =
         (size_t)plan.n_wg * mi::decode_record_floats(r0.head_dim, plan.group) * sizeof(float);
     if ((rc = ensure_workspace(rec_bytes))) return rc;
