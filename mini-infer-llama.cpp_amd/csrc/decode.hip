@@ -210,10 +210,10 @@ struct DecodeCfg {
   static constexpr int DEPF = HSL * (D + 2);      // floats of one wave's deposit
   static constexpr int REC = (DEPF + 3) & ~3;     // floats per record
   static constexpr int NE = D / 64;               // float4 column blocks per lane
-  // LDS layout (bytes)
+  // LDS layout (bytes). A wave's deposit overlays its own ring once the
+  // wave's last loads have landed.
   static constexpr int L_RING = 0;
-  static constexpr int L_DEP = L_RING + NWV * NB * SLOTB;
-  static constexpr int L_P = L_DEP + NWV * DEPF * 4;    // per wave: P[head slot][16]
+  static constexpr int L_P = L_RING + NWV * NB * SLOTB;  // per wave: P[head slot][16]
   static constexpr int L_FLAG = L_P + NWV * HSL * kDecodeSub * 4;
   static constexpr int L_ITEMS = L_FLAG + 16;
   static constexpr int L_TOTAL = L_ITEMS + kDecodeMaxItems * (int)sizeof(DecodeItem);
@@ -221,6 +221,7 @@ struct DecodeCfg {
   static_assert(NB >= 2, "ring depth");
   static_assert(SUBB % 1024 == 0, "1 KB load granularity");
   static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
+  static_assert(DEPF * 4 <= NB * SLOTB, "a deposit fits its wave's ring");
   // vmcnt allowed while waiting for a slot's K (its V and the later slots may
   // still be in flight) and for its V.
   static constexpr int WAIT_K = NDK + NDMA * (NB - 1);
@@ -482,12 +483,14 @@ void decode_kernel(const DecodeParams p) {
     }
   }
 
-  // The waves meet in LDS.
-  float* const dep = reinterpret_cast<float*>(lds_dyn + C::L_DEP);
+  // The waves meet in LDS: wave w's deposit at the start of its ring, once
+  // its last loads (including the zero-filling ones past the share) landed.
+  wait_vmem<0>();
+  auto dep_at = [&](int w) { return reinterpret_cast<float*>(lds_dyn + C::L_RING + w * NB * C::SLOTB); };
 #pragma unroll
   for (int h = 0; h < HS; ++h) l[h] = row_sum16(l[h]);
   {
-    float* dw = dep + wv * C::DEPF;
+    float* dw = dep_at(wv);
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
 #pragma unroll
@@ -509,12 +512,12 @@ void decode_kernel(const DecodeParams p) {
     if (t < SPW && hs < HSL) {
       float mx = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, dep[w * C::DEPF + HSL * D + 2 * hs]);
+      for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, dep_at(w)[HSL * D + 2 * hs]);
       float lt = 0.f;
       f32x4 at = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NWV; ++w) {
-        const float* dw = dep + w * C::DEPF;
+        const float* dw = dep_at(w);
         const float mw = dw[HSL * D + 2 * hs];
         const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);  // a wave with no sub-tile
         lt += wt * dw[HSL * D + 2 * hs + 1];
@@ -536,7 +539,7 @@ void decode_kernel(const DecodeParams p) {
       }
     }
   }
-  wait_vmem<0>();  // no LDS DMA outlives the workgroup; record stores have completed
+  wait_vmem<0>();  // the record stores have completed
   if (kpg == 1) return;
 
   // Cross-workgroup combine. The group's workgroups form teams of up to TEAM
@@ -659,7 +662,8 @@ void decode_kernel(const DecodeParams p) {
 }
 
 // Waves per workgroup: two per SIMD at head_dim 64 (a 128 KB ring still gives
-// every wave two slots), one per SIMD at head_dim 128.
+// every wave two slots), one per SIMD at head_dim 128 (eight waves measured no
+// faster there with an F16 cache: those launches are bound by latency).
 template <int D, typename KT>
 constexpr int decode_waves() {
   return D == 64 ? 8 : 4;
@@ -683,12 +687,15 @@ static hipError_t launch_decode_h(const DecodeParams& p, int group, hipStream_t 
   return group > 4 ? launch_decode_t<D, KT, 2>(p, stream) : launch_decode_t<D, KT, 1>(p, stream);
 }
 
-int decode_wg_waves(int head_dim) { return head_dim == 64 ? 8 : 4; }
+int decode_wg_waves(int head_dim, bool f16) {
+  (void)f16;
+  return head_dim == 64 ? 8 : 4;
+}
 
 // Records one merge round reads (the team size of the cross-workgroup combine).
-int decode_team(int head_dim, int group) {
+int decode_team(int head_dim, bool f16, int group) {
   const int hsl = group > 4 ? 8 : 4;
-  const int threads = decode_wg_waves(head_dim) * kWave;
+  const int threads = decode_wg_waves(head_dim, f16) * kWave;
   return threads / (hsl * head_dim / 4) * 8;
 }
 

@@ -12,9 +12,9 @@ namespace mi {
 
 // decode.hip
 int decode_group_size(int n_rep);                       // G: Q heads per group
-int decode_wg_waves(int head_dim);                      // waves per decode workgroup
+int decode_wg_waves(int head_dim, bool f16);            // waves per decode workgroup
 size_t decode_record_floats(int head_dim, int group);   // floats per cross-workgroup record
-int decode_team(int head_dim, int group);               // workgroups per combine team
+int decode_team(int head_dim, bool f16, int group);     // workgroups per combine team
 // p.rec / p.cnt: one record per workgroup and p.cst arrival counters per group
 // (zero on entry, left zero on exit).
 hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,

@@ -147,12 +147,13 @@ struct DecodePlan {
   int n_wg = 0;
 };
 
-DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim) {
+DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim,
+                       bool f16) {
   DecodePlan p;
   p.group = mi::decode_group_size(n_rep);
   p.n_chunks = n_rep / p.group;
   const int gpi = n_head_kv * p.n_chunks;
-  const int waves = mi::decode_wg_waves(head_dim);
+  const int waves = mi::decode_wg_waves(head_dim, f16);
   int64_t sub = 0;
   for (int i = 0; i < n_items; ++i) {
     it[i].spg = (it[i].n_kv + mi::kDecodeSub - 1) / mi::kDecodeSub;
@@ -328,9 +329,10 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
         return fail(MI_HIP_E_UNSUPPORTED,
                     "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + cnt);
     }
-    const DecodePlan plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim);
+    const DecodePlan plan =
+        plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16);
     // arrival counters: one per combine team plus one per group
-    const int team = mi::decode_team(r0.head_dim, plan.group);
+    const int team = mi::decode_team(r0.head_dim, r0.f16, plan.group);
     int max_kpg = 1;
     for (int i = 0; i < cnt; ++i) max_kpg = std::max(max_kpg, (int)p.item[i].kpg);
     p.cst = 1 + (max_kpg + team - 1) / team;
