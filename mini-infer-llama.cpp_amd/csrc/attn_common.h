@@ -96,6 +96,21 @@ __device__ inline void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Loads and stores through the global address space. Pointers that reach a
+// kernel through LDS (a staged argument table) are otherwise generic, and a
+// generic (flat) access counts against both the vector-memory and the LDS
+// counters, so every later LDS wait would also wait for it.
+template <typename T>
+__device__ __forceinline__ T gload(const void* p) {
+  typedef const __attribute__((address_space(1))) T gT;
+  return *(gT*)p;
+}
+template <typename T>
+__device__ __forceinline__ void gstore(void* p, T v) {
+  typedef __attribute__((address_space(1))) T gT;
+  *(gT*)p = v;
+}
+
 // LDS rows of NSLOT 16-byte slots: logical slot j of row r is stored at
 // physical slot j ^ swz(r), so 16 lanes reading one slot of 16 consecutive
 // rows hit distinct banks.

@@ -293,7 +293,7 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < NE; ++e) {
         const int hs = min(hb + 4 * h, G - 1);
-        const f32x4 q4 = *reinterpret_cast<const f32x4*>(q0 + (int64_t)hs * q_s1 + 4 * (64 * e + 4 * col));
+        const f32x4 q4 = gload<f32x4>(q0 + (int64_t)hs * q_s1 + 4 * (64 * e + 4 * col));
         qv[h][e][0] = q4.x; qv[h][e][1] = q4.y; qv[h][e][2] = q4.z; qv[h][e][3] = q4.w;
       }
   }
@@ -527,7 +527,7 @@ void decode_kernel(const DecodeParams p) {
         if (hs < G) {
           float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) +
                                               (int64_t)(head0 + hs) * o_s1);
-          *reinterpret_cast<f32x4*>(o + 4 * cq) = at * (1.f / lt);
+          gstore<f32x4>(o + 4 * cq, at * (1.f / lt));
         }
       } else {
         const unsigned r0 = (unsigned)(wg * C::REC * 4);
@@ -634,7 +634,7 @@ void decode_kernel(const DecodeParams p) {
   auto write_out = [&](float lt, f32x4 at) __attribute__((always_inline)) {
     if (sub == 0 && hs < G) {
       float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
-      *reinterpret_cast<f32x4*>(o + 4 * cq) = at * (1.f / lt);
+      gstore<f32x4>(o + 4 * cq, at * (1.f / lt));
     }
   };
 

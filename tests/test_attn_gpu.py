@@ -87,6 +87,26 @@ def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d):
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F32)
 
 
+def test_decode_back_to_back_launches_share_no_records(hip, stream, oracle):
+    # Two launches of one shape on one stream, no synchronisation between them:
+    # they use the same cross-workgroup record slots, and the second must merge
+    # only its own records (a record of the first launch carries an older stamp).
+    import torch
+    n_kv = 4096
+    runs = []
+    for seed in (71, 72):
+        q, k, v = cpu_attention.make_inputs(seed, 64, 14, 2, n_kv, 1)
+        out = torch.full(q.shape, float("nan"), dtype=torch.float32, device="cuda")
+        dq, dk, dv = dev(q), dev(k), dev(v)
+        runs.append((q, k, v, out, dq, dk, dv))
+    for q, k, v, out, dq, dk, dv in runs:
+        a = mh.attn_args(dq, out, 7, n_kv - 1, 0.125, stream, k=dk, v=dv)
+        hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+    torch.cuda.synchronize()
+    for i, (q, k, v, out, *_rest) in enumerate(runs):
+        assert_close(out.cpu().numpy(), ref_out(oracle, q, k, v, n_kv - 1, 0.125), TOL_F32, f"launch {i}")
+
+
 def test_decode_qwen7b_shape_f16_cache(hip, stream, oracle):
     n_kv = 8192
     q, k, v = cpu_attention.make_inputs(1238, 128, 28, 4, n_kv, 1)
