@@ -68,6 +68,7 @@ struct PrefillParams {
   int64_t o_s1, o_s2;
   int32_t n_head, n_rep, n_past, n_tokens;
   int32_t n_qblocks;     // ceil(n_tokens / 32)
+  int32_t lone;          // 1: the last query block has a workgroup of its own
   float scale_log2e;
 };
 

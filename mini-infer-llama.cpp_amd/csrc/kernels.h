@@ -21,7 +21,8 @@ hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int grou
                          hipStream_t stream);
 
 // prefill.hip
-hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, hipStream_t stream);
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu,
+                          hipStream_t stream);
 
 // nodes.hip -- node-level kernels on device tensors (byte strides).
 struct NodeView {

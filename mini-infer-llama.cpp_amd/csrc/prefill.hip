@@ -140,10 +140,14 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   const int col = lane & 31;
   const int kh = lane >> 5;
 
-  // workgroup -> (head h, query blocks qa and qz)
+  // workgroup -> (head h, query blocks qa and qz): pairs (j, NQ - 1 - j), or
+  // with p.lone the last block alone and then pairs (j, NQ - 2 - j). A lone
+  // middle block has qz == qa.
   const int h = blockIdx.x % p.n_head;
-  const int qa = blockIdx.x / p.n_head;
-  const int qz = p.n_qblocks - 1 - qa;
+  const int j = blockIdx.x / p.n_head;
+  const bool last_alone = p.lone && j == 0;
+  const int qa = last_alone ? p.n_qblocks - 1 : j - p.lone;
+  const int qz = last_alone ? qa : p.n_qblocks - 1 - p.lone - qa;
   const int n_kv = p.n_past + p.n_tokens;
   auto tiles = [&](int i) {
     return (min(n_kv, p.n_past + kPrefillRows * (i + 1)) + kPrefillKeys - 1) / kPrefillKeys;
@@ -430,26 +434,63 @@ constexpr int prefill_waves() {
   return D == 64 ? 8 : 4;
 }
 
+// Workgroups per head for a pairing (lone = 0 or 1).
+static int prefill_wgs_per_head(int n_qblocks, int lone) {
+  return lone + (n_qblocks - lone + 1) / 2;
+}
+
+// The pairing whose longest workgroup runs shortest: launch rounds on n_cu
+// CUs times the units of the longest workgroup per SIMD (the matrix cores
+// bound a unit; the waves of a workgroup share its CU's four SIMDs). At
+// n_past = 0 pairs (j, NQ - 1 - j) give NQ + 1 units, the lone-last pairing
+// NQ: with eight waves that is 8.25 against 8 units per SIMD.
+static int prefill_choose_lone(const PrefillParams& p, int n_cu) {
+  const int n_kv = p.n_past + p.n_tokens;
+  auto tiles = [&](int i) {
+    return (std::min(n_kv, p.n_past + kPrefillRows * (i + 1)) + kPrefillKeys - 1) / kPrefillKeys;
+  };
+  int64_t best = -1;
+  int best_lone = 0;
+  for (int lone = 0; lone <= (p.n_qblocks > 1 ? 1 : 0); ++lone) {
+    const int per_head = prefill_wgs_per_head(p.n_qblocks, lone);
+    int umax = 0;
+    for (int j = 0; j < per_head; ++j) {
+      const bool alone = lone && j == 0;
+      const int qa = alone ? p.n_qblocks - 1 : j - lone;
+      const int qz = alone ? qa : p.n_qblocks - 1 - lone - qa;
+      umax = std::max(umax, tiles(qa) + (qz != qa ? tiles(qz) : 0));
+    }
+    const int64_t wgs = (int64_t)p.n_head * per_head;
+    const int64_t cost = (wgs + n_cu - 1) / n_cu * ((umax + 3) / 4);
+    if (best < 0 || cost < best) {
+      best = cost;
+      best_lone = lone;
+    }
+  }
+  return best_lone;
+}
+
 template <int D, typename KT>
-static hipError_t launch_prefill_t(const PrefillParams& p, hipStream_t stream) {
+static hipError_t launch_prefill_t(PrefillParams p, int n_cu, hipStream_t stream) {
   constexpr int NW = prefill_waves<D>();
   typedef PrefillCfg<D, KT, NW> C;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<D, KT, NW>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
   if (attr != hipSuccess) return attr;
-  const unsigned n_pairs = (unsigned)((p.n_qblocks + 1) / 2);
-  hipLaunchKernelGGL((prefill_kernel<D, KT, NW>), dim3((unsigned)p.n_head * n_pairs),
+  p.lone = prefill_choose_lone(p, n_cu);
+  const unsigned per_head = (unsigned)prefill_wgs_per_head(p.n_qblocks, p.lone);
+  hipLaunchKernelGGL((prefill_kernel<D, KT, NW>), dim3((unsigned)p.n_head * per_head),
                      dim3(NW * kWave), C::LDS, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, hipStream_t stream) {
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu, hipStream_t stream) {
   if (head_dim == 64)
-    return f16 ? launch_prefill_t<64, _Float16>(p, stream) : launch_prefill_t<64, float>(p, stream);
+    return f16 ? launch_prefill_t<64, _Float16>(p, n_cu, stream) : launch_prefill_t<64, float>(p, n_cu, stream);
   if (head_dim == 128)
-    return f16 ? launch_prefill_t<128, _Float16>(p, stream)
-               : launch_prefill_t<128, float>(p, stream);
+    return f16 ? launch_prefill_t<128, _Float16>(p, n_cu, stream)
+               : launch_prefill_t<128, float>(p, n_cu, stream);
   return hipErrorInvalidValue;
 }
 

@@ -386,7 +386,7 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   p.n_tokens = a->n_tokens;
   p.n_qblocks = (a->n_tokens + mi::kPrefillRows - 1) / mi::kPrefillRows;
   p.scale_log2e = a->scale * kLog2e;
-  hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, stream);
+  hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, g.n_cu, stream);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   return MI_HIP_OK;
 }
