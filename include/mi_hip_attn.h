@@ -186,6 +186,45 @@ int mi_hip_op_attn_kqv(mi_tensor* dst, void* stream);
  * dst->src[0] the SOFTMAX node, dst->src[0]->src[0] the ATTN_QK node. */
 int mi_hip_op_attn_fused(mi_tensor* dst, void* stream);
 
+/* MI_OP_ROPE (src/ops_cpu.cpp:270-302; builder src/graph.cpp:146-154,
+ * op_params n_past, n_dims, freq_base): rotary embedding of dst->src[0]
+ * [head_dim, n_heads, n_tokens] into dst (may be the same memory), NEOX
+ * halves (element p pairs with p + n_dims/2), token i at position n_past + i.
+ * The frequencies base^(-2p/n_dims) are the host's powf values, as in the
+ * engine; the angle's cosine and sine are computed on the device. n_dims must
+ * be even, at most head_dim and at most 256. */
+int mi_hip_op_rope(mi_tensor* dst, void* stream);
+
+/* ---- the step before attention: RoPE and the KV append, fused ---------- */
+
+/* One layer's qh_rot = rope(qh); kh_rot = rope(kh); cpy(kh_rot -> cache K
+ * rows [n_past, n_past + n_tokens)); cpy(vh -> cache V rows) of
+ * src/model_qwen2.cpp:153-159, in one launch on device tensors, so Q, K and
+ * V never pass through host memory. Shapes [head_dim, heads, n_tokens] with
+ * byte strides nb[0..2] (q/q_out: n_head heads, k/v: the cache's n_head_kv).
+ * q may be NULL (no Q); q_out may equal q. F16 caches round K and V to
+ * nearest even, like mi_hip_kv_write. */
+typedef struct mi_hip_rope_args {
+  mi_hip_kv* kv;
+  int32_t layer;
+  int32_t n_past;
+  int32_t n_tokens;
+  int32_t n_dims;   /* rotated dims (even, <= head_dim), op_params[1] of ROPE */
+  float freq_base;  /* op_params[2] of ROPE */
+  int32_t n_head;   /* Q heads */
+  const float* q;
+  size_t q_nb[3];
+  float* q_out;
+  size_t q_out_nb[3];
+  const float* k;
+  size_t k_nb[3];
+  const float* v;
+  size_t v_nb[3];
+  void* stream;
+} mi_hip_rope_args;
+
+int mi_hip_rope_append(const mi_hip_rope_args* args);
+
 /* ---- executor hook for host-resident graphs ------------------------------ */
 
 /* Plans one step's graph (call after the allocator assigned data, before

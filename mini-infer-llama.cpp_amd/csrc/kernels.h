@@ -37,6 +37,31 @@ hipError_t launch_softmax_node(const NodeView& dst, const NodeView& src, int n_p
 hipError_t launch_attn_kqv_node(const NodeView& dst, const NodeView& probs, const NodeView& v,
                                 bool v_f16, int n_rep, hipStream_t stream);
 
+// rope.hip. freq[p] = base^(-2p / n_dims) as the host's powf computes it.
+constexpr int kRopeMaxPairs = 128;  // n_dims <= 256
+struct RopeNode {
+  const char* src;
+  char* dst;
+  int64_t src_nb[3], dst_nb[3];
+  int64_t rows;  // n_heads * n_tokens
+  int32_t n_heads, head_dim, n_past, n_dims;
+  float freq[kRopeMaxPairs];
+};
+struct RopeAppend {
+  const char* q;  // may be null
+  char* q_out;
+  const char* k;
+  const char* v;
+  char* k_cache;  // the layer's K and V tensors (position stride c_s2, head stride c_s1)
+  char* v_cache;
+  int64_t q_nb[3], qo_nb[3], k_nb[3], v_nb[3];
+  int64_t c_s1, c_s2;
+  int32_t n_tokens, n_head, n_head_kv, head_dim, n_past, n_dims;
+  float freq[kRopeMaxPairs];
+};
+hipError_t launch_rope_node(const RopeNode& p, hipStream_t stream);
+hipError_t launch_rope_append(const RopeAppend& p, bool f16, hipStream_t stream);
+
 // Cache append: src F32 [head_dim, n_head_kv, n_tokens] (device, byte strides)
 // into dst rows [pos0, pos0 + n_tokens) of a [head_dim, n_head_kv, n_ctx]
 // cache with byte strides dst_s1 (head) and dst_s2 (position).

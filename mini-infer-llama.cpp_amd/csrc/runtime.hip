@@ -839,6 +839,107 @@ int mi_hip_op_softmax(mi_tensor* dst, void* stream) {
   return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "softmax launch");
 }
 
+namespace {
+
+// freq[p] = base^(-2p / n_dims) for p < n_dims / 2, each a float powf exactly
+// as src/ops_cpu.cpp:289 evaluates it (the device then forms pos * freq[p]
+// with one rounded product, as the engine does).
+void rope_freqs(float* freq, int n_dims, float base) {
+  for (int p = 0; p < n_dims / 2; ++p) freq[p] = std::pow(base, -(float)(2 * p) / (float)n_dims);
+}
+
+int check_rope_dims(int n_dims, int head_dim) {
+  if (n_dims < 0 || n_dims % 2 || n_dims > head_dim || n_dims > 2 * mi::kRopeMaxPairs)
+    return fail(MI_HIP_E_UNSUPPORTED, "n_dims %d: must be even, in [0, head_dim = %d] and <= %d",
+                n_dims, head_dim, 2 * mi::kRopeMaxPairs);
+  return MI_HIP_OK;
+}
+
+bool strides4(const size_t nb[3]) { return nb[0] % 4 == 0 && nb[1] % 4 == 0 && nb[2] % 4 == 0; }
+
+}  // namespace
+
+int mi_hip_op_rope(mi_tensor* dst, void* stream) {
+  if (!dst || dst->op != MI_OP_ROPE) return fail(MI_HIP_E_INVALID, "dst is not a ROPE node");
+  const mi_tensor* s = dst->src[0];
+  int rc;
+  if ((rc = check_f32(dst, "dst")) || (rc = check_f32(s, "src"))) return rc;
+  for (int i = 0; i < 3; ++i)
+    if (dst->ne[i] != s->ne[i]) return fail(MI_HIP_E_INVALID, "ROPE shape differs from its source");
+  if (!strides4(dst->nb) || !strides4(s->nb))
+    return fail(MI_HIP_E_INVALID, "ROPE strides must be multiples of 4 bytes");
+  const int n_past = mi_tensor_param_i32(dst, 0), n_dims = mi_tensor_param_i32(dst, 1);
+  if (s->ne[0] > INT32_MAX || s->ne[1] > INT32_MAX || s->ne[2] > INT32_MAX)
+    return fail(MI_HIP_E_UNSUPPORTED, "ROPE extents beyond 2^31");
+  if ((rc = check_rope_dims(n_dims, (int)s->ne[0]))) return rc;
+  if (n_past < 0 || (int64_t)n_past + s->ne[2] > INT32_MAX)
+    return fail(MI_HIP_E_INVALID, "positions n_past + token must lie in [0, 2^31)");
+  mi::RopeNode p{};
+  p.src = static_cast<const char*>(s->data);
+  p.dst = static_cast<char*>(dst->data);
+  for (int i = 0; i < 3; ++i) {
+    p.src_nb[i] = (int64_t)s->nb[i];
+    p.dst_nb[i] = (int64_t)dst->nb[i];
+  }
+  p.rows = s->ne[1] * s->ne[2];
+  p.n_heads = (int32_t)s->ne[1];
+  p.head_dim = (int32_t)s->ne[0];
+  p.n_past = n_past;
+  p.n_dims = n_dims;
+  rope_freqs(p.freq, n_dims, mi_tensor_param_f32(dst, 2));
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_rope_node(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "rope launch");
+}
+
+int mi_hip_rope_append(const mi_hip_rope_args* a) {
+  if (!a || !a->kv || !a->k || !a->v) return fail(MI_HIP_E_INVALID, "args, kv, k and v must be non-NULL");
+  const mi_hip_kv* kv = a->kv;
+  if (a->layer < 0 || a->layer >= kv->d.n_layer)
+    return fail(MI_HIP_E_INVALID, "layer %d out of range [0, %d)", a->layer, kv->d.n_layer);
+  if (a->n_past < 0 || a->n_tokens < 0 || (int64_t)a->n_past + a->n_tokens > kv->d.n_ctx)
+    return fail(MI_HIP_E_INVALID, "positions [%d, %d) outside [0, %d)", a->n_past,
+                a->n_past + a->n_tokens, kv->d.n_ctx);
+  int rc;
+  if ((rc = check_rope_dims(a->n_dims, kv->d.head_dim))) return rc;
+  if (a->q) {
+    if (!a->q_out) return fail(MI_HIP_E_INVALID, "q_out is NULL");
+    if (a->n_head <= 0 || a->n_head % kv->d.n_head_kv)
+      return fail(MI_HIP_E_INVALID, "n_head %d must be a positive multiple of n_head_kv %d",
+                  a->n_head, kv->d.n_head_kv);
+    if (!strides4(a->q_nb) || !strides4(a->q_out_nb))
+      return fail(MI_HIP_E_INVALID, "Q strides must be multiples of 4 bytes");
+  }
+  if (!strides4(a->k_nb) || !strides4(a->v_nb))
+    return fail(MI_HIP_E_INVALID, "K/V strides must be multiples of 4 bytes");
+  if (a->n_tokens == 0) return MI_HIP_OK;
+  mi::RopeAppend p{};
+  p.q = reinterpret_cast<const char*>(a->q);
+  p.q_out = reinterpret_cast<char*>(a->q_out);
+  p.k = reinterpret_cast<const char*>(a->k);
+  p.v = reinterpret_cast<const char*>(a->v);
+  p.k_cache = kv->tensor(a->layer, 0);
+  p.v_cache = kv->tensor(a->layer, 1);
+  for (int i = 0; i < 3; ++i) {
+    p.q_nb[i] = (int64_t)a->q_nb[i];
+    p.qo_nb[i] = (int64_t)a->q_out_nb[i];
+    p.k_nb[i] = (int64_t)a->k_nb[i];
+    p.v_nb[i] = (int64_t)a->v_nb[i];
+  }
+  p.c_s1 = kv->s1;
+  p.c_s2 = kv->s2;
+  p.n_tokens = a->n_tokens;
+  p.n_head = a->q ? a->n_head : 0;
+  p.n_head_kv = kv->d.n_head_kv;
+  p.head_dim = kv->d.head_dim;
+  p.n_past = a->n_past;
+  p.n_dims = a->n_dims;
+  rope_freqs(p.freq, a->n_dims, a->freq_base);
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_rope_append(p, kv->elt == 2, static_cast<hipStream_t>(a->stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "rope append launch");
+}
+
 int mi_hip_op_attn_kqv(mi_tensor* dst, void* stream) {
   if (!dst || dst->op != MI_OP_ATTN_KQV) return fail(MI_HIP_E_INVALID, "dst is not an ATTN_KQV node");
   const mi_tensor* pr = dst->src[0];

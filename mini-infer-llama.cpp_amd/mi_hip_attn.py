@@ -15,6 +15,7 @@ MI_TYPE_F32 = 0
 MI_TYPE_F16 = 1
 
 MI_OP_NONE = 0
+MI_OP_ROPE = 6
 MI_OP_SOFTMAX = 7
 MI_OP_CPY = 10
 MI_OP_VIEW = 13
@@ -96,6 +97,27 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class RopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("kv", ctypes.c_void_p),
+        ("layer", ctypes.c_int32),
+        ("n_past", ctypes.c_int32),
+        ("n_tokens", ctypes.c_int32),
+        ("n_dims", ctypes.c_int32),
+        ("freq_base", ctypes.c_float),
+        ("n_head", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("q_nb", ctypes.c_size_t * 3),
+        ("q_out", ctypes.c_void_p),
+        ("q_out_nb", ctypes.c_size_t * 3),
+        ("k", ctypes.c_void_p),
+        ("k_nb", ctypes.c_size_t * 3),
+        ("v", ctypes.c_void_p),
+        ("v_nb", ctypes.c_size_t * 3),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
 class AllocStats(ctypes.Structure):
     _fields_ = [("n_malloc", ctypes.c_uint64), ("n_free", ctypes.c_uint64),
                 ("bytes_live", ctypes.c_uint64), ("bytes_peak", ctypes.c_uint64)]
@@ -123,6 +145,8 @@ SIGNATURES = {
     "mi_hip_op_softmax": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_op_attn_kqv": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_op_attn_fused": ([ctypes.POINTER(MiTensor), _P], _I),
+    "mi_hip_op_rope": ([ctypes.POINTER(MiTensor), _P], _I),
+    "mi_hip_rope_append": ([ctypes.POINTER(RopeArgs)], _I),
     "mi_hip_graph_prepare": ([ctypes.POINTER(MiCgraph)], _I),
     "mi_hip_compute_forward": ([ctypes.POINTER(MiTensor), _I, _I], _I),
 }
@@ -219,6 +243,26 @@ def attn_args(q, out, n_rep, n_past, scale, stream, kv=None, layer=0, k=None, v=
     a.n_rep = n_rep
     a.n_past = n_past
     a.scale = scale
+    a.stream = stream
+    return a
+
+
+def rope_args(kv, layer, n_past, n_dims, freq_base, stream, k, v, q=None, q_out=None):
+    """Builds RopeArgs from torch tensors shaped (n_tokens, heads, head_dim): k/v
+    with the cache's n_head_kv heads, q/q_out (optional) with n_head heads."""
+    a = RopeArgs()
+    a.kv, a.layer, a.n_past, a.n_dims = kv, layer, n_past, n_dims
+    a.freq_base = freq_base
+    a.n_tokens = k.shape[0]
+    a.k, a.v = k.data_ptr(), v.data_ptr()
+    a.k_nb[:] = nb3_of(k)
+    a.v_nb[:] = nb3_of(v)
+    if q is not None:
+        q_out = q if q_out is None else q_out
+        a.q, a.q_out = q.data_ptr(), q_out.data_ptr()
+        a.q_nb[:] = nb3_of(q)
+        a.q_out_nb[:] = nb3_of(q_out)
+        a.n_head = q.shape[1]
     a.stream = stream
     return a
 

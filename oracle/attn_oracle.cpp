@@ -13,6 +13,8 @@
 //   MI_OP_SOFTMAX       src/ops_cpu.cpp:304-346
 //   MI_OP_ATTN_QK       src/ops_cpu.cpp:356-380
 //   MI_OP_ATTN_KQV      src/ops_cpu.cpp:386-410
+//   MI_OP_ROPE          src/ops_cpu.cpp:270-302 (NEOX halves; op_params of
+//                       src/graph.cpp:146-154)
 //   F16 -> F32          src/quant.cpp:26-63 (IEEE binary16 widening)
 // Build flags: -O3 -ffp-contract=off, no -ffast-math, no -march: the same
 // scalar float semantics as the reference's baseline x86-64 build.
@@ -127,6 +129,39 @@ void attn_kqv(mi_tensor* dst, int ith, int nth) {
       for (int64_t t = 0; t < n_key; ++t) acc += elem(v, o, g, t) * elem(p, t, j, h);
       elem(dst, o, h, j) = acc;
     }
+  }
+}
+
+// Rotary position embedding, NEOX form: for each row (head i1, token i2) at
+// position n_past + i2 and each p < n_dims / 2, the pair (p, p + n_dims / 2)
+// is rotated by theta = pos * base^(-2p / n_dims), all in float: the
+// frequency from powf, the angle one float product, cosf/sinf, and the
+// rotation as two rounded products and one rounded sum or difference.
+// Elements from n_dims on are copied. Rows split over threads like every
+// other node (src/ops_cpu.cpp:270-302).
+void rope(mi_tensor* dst, int ith, int nth) {
+  const mi_tensor* src = dst->src[0];
+  int32_t n_past, n_dims;
+  float base;
+  std::memcpy(&n_past, &dst->op_params[0], 4);
+  std::memcpy(&n_dims, &dst->op_params[1], 4);
+  std::memcpy(&base, &dst->op_params[2], 4);
+  const int64_t head_dim = src->ne[0], n_heads = src->ne[1];
+  const int64_t half = n_dims / 2;
+  int64_t lo, hi;
+  share_of(n_heads * src->ne[2], ith, nth, &lo, &hi);
+  for (int64_t r = lo; r < hi; ++r) {
+    const int64_t i1 = r % n_heads, i2 = r / n_heads;
+    const int64_t pos = n_past + i2;
+    for (int64_t p = 0; p < half; ++p) {
+      const float freq = powf(base, -(float)(2 * p) / (float)n_dims);
+      const float theta = (float)pos * freq;
+      const float c = cosf(theta), sn = sinf(theta);
+      const float x0 = elem(src, p, i1, i2), x1 = elem(src, p + half, i1, i2);
+      elem(dst, p, i1, i2) = x0 * c - x1 * sn;
+      elem(dst, p + half, i1, i2) = x0 * sn + x1 * c;
+    }
+    for (int64_t i = n_dims; i < head_dim; ++i) elem(dst, i, i1, i2) = elem(src, i, i1, i2);
   }
 }
 
@@ -258,6 +293,21 @@ void oracle_split_range(int64_t n, int ith, int nth, int64_t* lo, int64_t* hi) {
 void oracle_attn_qk(mi_tensor* dst, int ith, int nth) { attn_qk(dst, ith, nth); }
 void oracle_softmax(mi_tensor* dst, int ith, int nth) { softmax(dst, ith, nth); }
 void oracle_attn_kqv(mi_tensor* dst, int ith, int nth) { attn_kqv(dst, ith, nth); }
+void oracle_rope_node(mi_tensor* dst, int ith, int nth) { rope(dst, ith, nth); }
+
+// MI_OP_ROPE on contiguous [head_dim, n_head, n_tokens] buffers, one thread.
+void oracle_rope(const float* src, float* dst, int head_dim, int n_head, int n_tokens, int n_past,
+                 int n_dims, float freq_base) {
+  mi_tensor s, d;
+  set_contiguous(&s, head_dim, n_head, n_tokens, const_cast<float*>(src));
+  set_contiguous(&d, head_dim, n_head, n_tokens, dst);
+  d.op = MI_OP_ROPE;
+  d.src[0] = &s;
+  std::memcpy(&d.op_params[0], &n_past, 4);
+  std::memcpy(&d.op_params[1], &n_dims, 4);
+  std::memcpy(&d.op_params[2], &freq_base, 4);
+  rope(&d, 0, 1);
+}
 
 // IEEE binary16 -> binary32, exact for every input (src/quant.cpp:26-63):
 // zero, subnormal (renormalised), normal, inf and nan payloads.

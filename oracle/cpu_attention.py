@@ -111,6 +111,16 @@ class Oracle(CpuAttention):
                                                 ctypes.POINTER(ctypes.c_int64),
                                                 ctypes.POINTER(ctypes.c_int64)]
 
+    def rope(self, x, n_past, n_dims, freq_base):
+        """MI_OP_ROPE of x shaped (n_tokens, n_head, head_dim), one thread."""
+        x = np.ascontiguousarray(x, np.float32)
+        t, h, d = x.shape
+        y = np.empty_like(x)
+        fn = self.lib.oracle_rope
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 5 + [ctypes.c_float]
+        fn(x.ctypes.data, y.ctypes.data, d, h, t, n_past, n_dims, ctypes.c_float(freq_base))
+        return y
+
     def split_range(self, n, ith, nth):
         lo, hi = ctypes.c_int64(), ctypes.c_int64()
         self.lib.oracle_split_range(n, ith, nth, ctypes.byref(lo), ctypes.byref(hi))

@@ -102,6 +102,24 @@ int ref_softmax(const float* src, float* dst, int n_kv, int n_tokens, int n_head
   return 0;
 }
 
+// Reference MI_OP_ROPE (src/graph.cpp:146-154 builder, src/ops_cpu.cpp:270-302
+// kernel) on a contiguous [head_dim, n_head, n_tokens] input, one thread.
+int ref_rope(const float* src, float* dst, int head_dim, int n_head, int n_tokens, int n_past,
+             int n_dims, float freq_base) {
+  mi_context_params cp{};
+  cp.tensor_capacity = 4;
+  cp.data_capacity = 0;
+  cp.no_alloc = true;
+  mi_context* ctx = mi_context_new(cp);
+  int64_t ne[3] = {head_dim, n_head, n_tokens};
+  mi_tensor* s = mi_context_new_tensor_from_data(ctx, MI_TYPE_F32, 3, ne, (void*)src);
+  mi_tensor* r = mi_graph_rope(ctx, s, n_past, n_dims, freq_base);
+  r->data = dst;
+  mi_compute_rope(r, 0, 1);
+  mi_context_free(ctx);
+  return 0;
+}
+
 float ref_fp16_to_fp32(uint16_t h) { return mi_fp16_to_fp32(h); }
 
 // The reference's own struct layout (src/tensor.h:122-160, src/graph.h:19-47),

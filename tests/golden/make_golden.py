@@ -55,6 +55,18 @@ CASES = {
 STORE_SCORES_MAX = 65536  # elements; larger cases keep only the output
 
 
+# name: (head_dim, n_head, n_tokens, n_past, n_dims, freq_base, fixed input or None)
+ROPE_CASES = {
+    "rope_kat_identity": (4, 1, 1, 0, 4, 10000.0, [1, 2, 3, 4]),  # test_ops_cpu.cpp:181-196
+    "rope_kat_rotation": (2, 1, 1, 5, 2, 10000.0, [1, 0]),        # test_ops_cpu.cpp:198-213
+    "rope_q_decode": (64, 14, 1, 511, 64, 1000000.0, None),        # Qwen2.5-0.5B decode Q
+    "rope_q_prefill": (64, 14, 40, 0, 64, 1000000.0, None),
+    "rope_k_chunk": (64, 2, 19, 13, 64, 1000000.0, None),          # a chunk after 13 tokens
+    "rope_7b_q_far": (128, 28, 2, 30000, 128, 1000000.0, None),    # large angles
+    "rope_partial": (64, 4, 3, 5, 32, 10000.0, None),              # n_dims < head_dim
+}
+
+
 def f16_lut(ref):
     import ctypes
     fn = ref.lib.ref_fp16_to_fp32_row
@@ -103,6 +115,25 @@ def main():
     fn(src.ctypes.data, dst.ctypes.data, 4, 2, 1, 0, ctypes.c_float(1.0))
     np.savez(os.path.join(OUT_DIR, "softmax_kat.npz"), src=src, probs=dst)
     manifest["softmax_kat"] = {"n_past": 0, "scale": 1.0, "sha256_probs": sha256(dst)}
+
+    # MI_OP_ROPE (src/ops_cpu.cpp:270-302): the known-answer cases of
+    # tests/test_ops_cpu.cpp:181-213 and the engine's Q/K shapes, inputs
+    # [n_tokens][n_head][head_dim] from a seeded generator, stored with them.
+    import ctypes
+    fn = ref.lib.ref_rope
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 5 + [ctypes.c_float]
+    rng = np.random.default_rng(4242)
+    manifest["rope"] = {}
+    for name, (d, h, t, n_past, n_dims, base, src) in ROPE_CASES.items():
+        x = (np.asarray(src, np.float32).reshape(t, h, d) if src is not None
+             else rng.standard_normal((t, h, d)).astype(np.float32))
+        y = np.empty_like(x)
+        fn(x.ctypes.data, y.ctypes.data, d, h, t, n_past, n_dims, ctypes.c_float(base))
+        np.savez(os.path.join(OUT_DIR, name + ".npz"), src=x, dst=y)
+        manifest["rope"][name] = {"head_dim": d, "n_head": h, "n_tokens": t, "n_past": n_past,
+                                  "n_dims": n_dims, "freq_base": base,
+                                  "sha256_src": sha256(x), "sha256_dst": sha256(y)}
+        print(f"{name}: {x.shape}")
 
     # The reference's F16 widening over every code, as float32 bit patterns.
     if lut is None:

@@ -3,6 +3,8 @@ public headers declare, agrees with the engine on the mi_tensor layout
 (src/tensor.h:122-160), and rejects bad arguments with status codes before it
 touches a device (src: the engine's asserts become errors here)."""
 import ctypes
+
+import numpy as np
 import os
 import re
 
@@ -99,6 +101,21 @@ def test_status_and_errors_without_device(lib):
     assert lib.mi_hip_op_attn_qk(ctypes.byref(t), None) == 1
     assert lib.mi_hip_op_attn_kqv(ctypes.byref(t), None) == 1
     assert lib.mi_hip_op_attn_fused(ctypes.byref(t), None) == 1
+    # ROPE: wrong node, odd or oversized n_dims, unaligned strides, no kv
+    assert lib.mi_hip_op_rope(ctypes.byref(t), None) == 1
+    buf = np.zeros(64, np.float32)
+    src = mh.make_tensor(buf.ctypes.data, [8, 2, 4], [4, 32, 64])
+    for n_dims, code in ((7, 5), (10, 5), (-2, 5), (300, 5)):
+        node = mh.make_tensor(buf.ctypes.data, [8, 2, 4], [4, 32, 64], op=mh.MI_OP_ROPE,
+                              src=[src], params=[0, n_dims, 10000.0])
+        assert lib.mi_hip_op_rope(ctypes.byref(node), None) == code, n_dims
+    src_bad = mh.make_tensor(buf.ctypes.data, [8, 2, 4], [4, 34, 64])
+    node = mh.make_tensor(buf.ctypes.data, [8, 2, 4], [4, 32, 64], op=mh.MI_OP_ROPE,
+                          src=[src_bad], params=[0, 8, 10000.0])
+    assert lib.mi_hip_op_rope(ctypes.byref(node), None) == 1
+    assert lib.mi_hip_rope_append(None) == 1
+    ra = mh.RopeArgs()
+    assert lib.mi_hip_rope_append(ctypes.byref(ra)) == 1 and "NULL" in lib.last_error()
     # A node that is not attention and not a KV write is not ours.
     t.op = 4  # ADD
     assert lib.mi_hip_compute_forward(ctypes.byref(t), 0, 1) == 0

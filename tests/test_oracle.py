@@ -7,7 +7,8 @@
 2. Mathematics the reference's output is fixed by, chosen so that a plausible
    slip (wrong GQA index, transposed operand, off-by-one mask, missing scale)
    fails: float64 brute force, one-hot known answers, invariants.
-3. The reference's own known-answer softmax test (tests/test_ops_cpu.cpp:215-241).
+3. The reference's own known-answer softmax test (tests/test_ops_cpu.cpp:215-241)
+   and rope tests (tests/test_ops_cpu.cpp:181-213).
 """
 import numpy as np
 import pytest
@@ -204,3 +205,78 @@ def test_invariants(oracle):
     s_c, _, _ = oracle.attention(q[:1], k, v, 47, 2.0, 1)
     assert np.array_equal(s_a, s_c)
     assert np.allclose(p_a, p_b, rtol=1e-5, atol=1e-7)
+
+
+# ---- MI_OP_ROPE (src/ops_cpu.cpp:270-302) -----------------------------------
+
+def test_rope_matches_reference_goldens_bitwise(oracle, golden_manifest):
+    for name, c in golden_manifest["rope"].items():
+        g = load_golden(name)
+        assert cpu_attention.sha256(g["src"]) == c["sha256_src"], name
+        assert cpu_attention.sha256(g["dst"]) == c["sha256_dst"], name
+        y = oracle.rope(g["src"], c["n_past"], c["n_dims"], c["freq_base"])
+        assert np.array_equal(bits(y), bits(g["dst"])), name
+
+
+def test_rope_known_answers_from_reference_tests(oracle):
+    # test_ops_cpu.cpp:181-196: position 0 is the identity for every pair.
+    x = np.array([[[1, 2, 3, 4]]], np.float32)
+    assert np.array_equal(oracle.rope(x, 0, 4, 10000.0), x)
+    # test_ops_cpu.cpp:198-213: one pair, frequency base^0 = 1, position 5.
+    y = oracle.rope(np.array([[[1, 0]]], np.float32), 5, 2, 10000.0)
+    assert abs(y[0, 0, 0] - np.cos(5.0)) < 1e-6 and abs(y[0, 0, 1] - np.sin(5.0)) < 1e-6
+
+
+def test_rope_pairs_halves_with_the_stated_frequencies(oracle):
+    # One-hot inputs: element p may only move to p + n_dims/2 (NEOX halves, not
+    # adjacent elements), by the angle pos * base^(-2p / n_dims) (float64 here).
+    d, n_dims, base, pos = 64, 48, 10000.0, 3
+    half = n_dims // 2
+    for p in (0, 1, 7, half - 1):
+        x = np.zeros((1, 1, d), np.float32)
+        x[0, 0, p] = 1.0
+        y = oracle.rope(x, pos, n_dims, base)[0, 0]
+        theta = pos * base ** (-2.0 * p / n_dims)
+        want = np.zeros(d)
+        want[p], want[p + half] = np.cos(theta), np.sin(theta)
+        assert np.abs(y - want).max() < 2e-6, p
+        x[0, 0, p] = 0.0
+        x[0, 0, p + half] = 1.0  # the partner turns the other way
+        y = oracle.rope(x, pos, n_dims, base)[0, 0]
+        want = np.zeros(d)
+        want[p], want[p + half] = -np.sin(theta), np.cos(theta)
+        assert np.abs(y - want).max() < 2e-6, p
+    # elements from n_dims on pass through unchanged
+    x = np.random.default_rng(3).standard_normal((2, 3, d)).astype(np.float32)
+    y = oracle.rope(x, 17, n_dims, base)
+    assert np.array_equal(y[..., n_dims:], x[..., n_dims:])
+
+
+def test_rope_rotations_keep_pair_norms_and_compose(oracle):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((4, 3, 64)).astype(np.float32)
+    y = oracle.rope(x, 100, 64, 1000000.0)
+    n0 = np.hypot(x[..., :32].astype(np.float64), x[..., 32:])
+    n1 = np.hypot(y[..., :32].astype(np.float64), y[..., 32:])
+    assert np.abs(n1 - n0).max() < 1e-5 * max(1.0, n0.max())
+    # token t of a call at n_past is position n_past + t: one call over four
+    # tokens equals four one-token calls
+    for t in range(4):
+        one = oracle.rope(x[t:t + 1], 100 + t, 64, 1000000.0)
+        assert np.array_equal(bits(one[0]), bits(y[t]))
+
+
+def test_rope_oracle_equals_reference_library(oracle):
+    ref = cpu_attention.reference()
+    if ref is None:
+        pytest.skip("oracle/_ref (the reference compiled in place) is not built")
+    import ctypes
+    fn = ref.lib.ref_rope
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 5 + [ctypes.c_float]
+    rng = np.random.default_rng(6)
+    for (d, h, t, n_past, n_dims, base) in [(64, 14, 9, 4000, 64, 1e6), (128, 4, 3, 65000, 128, 1e6),
+                                            (64, 2, 5, 0, 16, 500.0), (8, 3, 2, 7, 6, 10000.0)]:
+        x = rng.standard_normal((t, h, d)).astype(np.float32)
+        want = np.empty_like(x)
+        fn(x.ctypes.data, want.ctypes.data, d, h, t, n_past, n_dims, ctypes.c_float(base))
+        assert np.array_equal(bits(oracle.rope(x, n_past, n_dims, base)), bits(want))
