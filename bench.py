@@ -38,7 +38,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,prefill,d7b,perlayer,copy (copy: the counter "
+                    help="comma list: decode,prefill,d7b,perlayer,q8,copy (copy: the counter "
                          "calibration workload, only when named)")
     return ap.parse_args()
 
@@ -147,6 +147,48 @@ def bench_prefill(torch, mh, lib, stream, steps, warmup, n, h=14, hkv=2, d=64):
                 tflops=flops / (kern_ms * 1e-3) / 1e12)
 
 
+def q8_weight_tensor(torch, gen, n, k):
+    """Random Q8_0 weight rows on the device: fp16 scales in [1e-4, 4e-3), int8
+    values in [-127, 127], packed as the 34-byte GGUF blocks."""
+    nb = k // 32
+    blocks = torch.empty((n, nb, 34), dtype=torch.uint8, device="cuda")
+    scale = (torch.rand((n, nb), device="cuda", generator=gen) * 4e-3 + 1e-4).to(torch.float16)
+    blocks[:, :, :2] = scale.view(torch.uint8).view(n, nb, 2)
+    blocks[:, :, 2:] = torch.randint(-127, 128, (n, nb, 32), device="cuda", generator=gen,
+                                     dtype=torch.int8).view(torch.uint8)
+    return blocks.view(n, nb * 34)
+
+
+def bench_q8_matvec(torch, mh, lib, stream, steps, warmup, n=151936, k=896, sets=3):
+    """MUL_MAT with Q8_0 weights for one token: the output projection of
+    Qwen2.5-0.5B (151936 x 896, tied to the token embedding), the largest
+    matrix-vector product of a decode step; weight sets rotated beyond the
+    256 MB MALL. One QUANTIZE_Q8_0 of the activation, then timed MUL_MATs."""
+    gen = torch.Generator(device="cuda").manual_seed(151936)
+    ws = [q8_weight_tensor(torch, gen, n, k) for _ in range(sets)]
+    x = torch.randn((1, k), device="cuda", generator=gen)
+    act = torch.empty((k // 32 * 36,), dtype=torch.uint8, device="cuda")
+    out = torch.empty((1, n), device="cuda")
+    xt = mh.make_tensor(x.data_ptr(), [k, 1], [4, 4 * k])
+    qn = mh.make_tensor(act.data_ptr(), [k, 1], [36, k // 32 * 36], type_=mh.MI_TYPE_Q8_0_ACT,
+                        op=mh.MI_OP_QUANTIZE_Q8_0, src=[xt])
+    lib.check(lib.mi_hip_op_quantize_q8_0(ctypes.byref(qn), stream))
+    nodes = []
+    for w in ws:
+        wt = mh.make_tensor(w.data_ptr(), [k, n], [34, k // 32 * 34], type_=mh.MI_TYPE_Q8_0)
+        nodes.append((wt, mh.make_tensor(out.data_ptr(), [n, 1], [4, 4 * n],
+                                         op=mh.MI_OP_MUL_MAT, src=[wt, qn])))
+
+    def launch(i):
+        rc = lib.mi_hip_op_mul_mat(ctypes.byref(nodes[i % sets][1]), stream)
+        if rc:
+            raise mh.MiHipError(rc, lib.last_error())
+
+    ms = run_timed(torch, launch, steps, warmup)
+    nbytes = n * (k // 32 * 34) + k // 32 * 36 + 4 * n
+    return dict(n=n, k=k, kernel_ms=ms, bytes=nbytes, gbps=nbytes / (ms * 1e-3) / 1e9, sets=sets)
+
+
 def bench_copy(torch, steps, warmup, nbytes=256 << 20):
     """A plain device-to-device copy of known size: the calibration workload for
     the FETCH_SIZE / WRITE_SIZE counters (bytes read = bytes written = nbytes)."""
@@ -243,6 +285,11 @@ def main():
         print(f"# per-layer launches: {res['per_layer']['us_per_layer']:.2f} us/layer",
               file=sys.stderr, flush=True)
 
+    if want("q8"):
+        res["q8"] = bench_q8_matvec(torch, mh, lib, stream, args.steps, args.warmup)
+        print(f"# q8_0 matvec 151936x896: {res['q8']['gbps']:.1f} GB/s "
+              f"({res['q8']['kernel_ms'] * 1e3:.2f} us)", file=sys.stderr, flush=True)
+
     if "copy" in only:
         res["copy"] = bench_copy(torch, max(5, args.steps // 10), 2)
         print(f"# copy 256 MiB: {res['copy']['gbps']:.1f} GB/s (read + write)", file=sys.stderr,
@@ -287,6 +334,16 @@ def main():
     if cpu:
         out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                for k, v in cpu.items()}
+    if "q8" in res:
+        q8 = res["q8"]
+        out["q8_0_matvec"] = {
+            "metric": "MUL_MAT Q8_0 weights x 1 token GB/s (Qwen2.5-0.5B output projection, "
+                      "151936 x 896)",
+            "gbps": round(q8["gbps"], 2), "us": round(q8["kernel_ms"] * 1e3, 2),
+            "roofline": {"bound": "hbm", "achieved": round(q8["gbps"], 2), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(q8["gbps"] / HBM_PEAK_GBPS, 4),
+                         "bytes_per_launch": q8["bytes"]},
+        }
     if "prefill1024" in res:
         p1, p4 = res["prefill1024"], res["prefill4096"]
         out["prefill"] = {

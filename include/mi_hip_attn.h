@@ -195,6 +195,23 @@ int mi_hip_op_attn_fused(mi_tensor* dst, void* stream);
  * be even, at most head_dim and at most 256. */
 int mi_hip_op_rope(mi_tensor* dst, void* stream);
 
+/* ---- the step after attention: Q8_0 matrix-vector products -------------- */
+
+/* MI_OP_QUANTIZE_Q8_0 (src/ops_cpu.cpp:462-479, row quantizer
+ * src/quant.cpp:188-210; builder src/graph.cpp:117-128): dst (type
+ * MI_TYPE_Q8_0_ACT, blocks of a float scale and 32 int8) from an F32 src of
+ * the same ne[], each row contiguous (nb[0] = 4), ne[0] a multiple of 32.
+ * Bit-exact: amax/127 scale, round half to even, clamp to [-127, 127]. */
+int mi_hip_op_quantize_q8_0(mi_tensor* dst, void* stream);
+
+/* MI_OP_MUL_MAT with Q8_0 weights (src/ops_cpu.cpp:226-236; builder
+ * src/graph.cpp:130-144): dst [n, m] F32 = src[0] (MI_TYPE_Q8_0 [k, n], GGUF
+ * blocks, row i at nb[1] * i) times src[1] (MI_TYPE_Q8_0_ACT [k, m], column j
+ * at nb[1] * j), e.g. the attention output projection. Bit-exact with the
+ * reference's default dot product (src/quant_avx2.cpp:174-185). F32 and F16
+ * weights are not handled here (MI_HIP_E_UNSUPPORTED). */
+int mi_hip_op_mul_mat(mi_tensor* dst, void* stream);
+
 /* ---- the step before attention: RoPE and the KV append, fused ---------- */
 
 /* One layer's qh_rot = rope(qh); kh_rot = rope(kh); cpy(kh_rot -> cache K

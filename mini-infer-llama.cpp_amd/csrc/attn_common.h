@@ -112,6 +112,22 @@ __device__ __forceinline__ void gstore(void* p, T v) {
   *(gT*)p = v;
 }
 
+// Typed LDS accesses through the LDS address space (32-bit addresses).
+template <typename T>
+__device__ __forceinline__ T lds_load(const lds_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void lds_store(lds_t* p, T v) {
+  *reinterpret_cast<__attribute__((address_space(3))) T*>(p) = v;
+}
+// 16 bytes per lane from r + voff into LDS at lds + 16 * lane (buffer_load ...
+// lds). Kept out of templates: the host pass drops a kernel template whose
+// body names the builtin directly.
+__device__ inline void dma16(rsrc_t r, lds_t* lds, unsigned voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
+}
+
 // LDS rows of NSLOT 16-byte slots: logical slot j of row r is stored at
 // physical slot j ^ swz(r), so 16 lanes reading one slot of 16 consecutive
 // rows hit distinct banks.

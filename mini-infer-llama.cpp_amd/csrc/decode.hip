@@ -181,18 +181,7 @@ __device__ __forceinline__ void qk4(float (&s)[HS][4 / HS], const float (&q)[HS]
 #undef MI_NOP
 #undef MI_DPP
 
-template <typename T>
-__device__ __forceinline__ T lds_load(const lds_t* p) {
-  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(p);
-}
-template <typename T>
-__device__ __forceinline__ void lds_store(lds_t* p, T v) {
-  *reinterpret_cast<__attribute__((address_space(3))) T*>(p) = v;
-}
-// 16 bytes per lane from r + voff into LDS at lds + 16 * lane.
-__device__ inline void dma16(rsrc_t r, lds_t* lds, unsigned voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
-}
+
 
 template <int D, typename KT, int HS, int NWV>
 struct DecodeCfg {

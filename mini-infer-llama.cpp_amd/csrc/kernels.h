@@ -62,6 +62,24 @@ struct RopeAppend {
 hipError_t launch_rope_node(const RopeNode& p, hipStream_t stream);
 hipError_t launch_rope_append(const RopeAppend& p, bool f16, hipStream_t stream);
 
+// mul_mat.hip. Activation rows (F32, ne0 a multiple of 32, contiguous within
+// a row) -> Q8_0_ACT blocks; Q8_0 weight rows . activation columns -> F32.
+struct Q8Quantize {
+  const char* src;
+  char* dst;
+  int64_t src_nb[4], dst_nb[4];
+  int64_t ne0, ne1, ne2, rows;  // rows = ne1 * ne2 * ne3
+};
+struct Q8MulMat {
+  const char* w;  // n rows of k/32 34-byte blocks, row i at w_nb1 * i
+  const char* a;  // m columns of k/32 36-byte blocks, column j at a_nb1 * j
+  char* dst;      // dst(i, j) at dst_nb0 * i + dst_nb1 * j
+  int64_t w_nb1, a_nb1, dst_nb0, dst_nb1;
+  int64_t k, n, m;
+};
+hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream);
+hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream);
+
 // Cache append: src F32 [head_dim, n_head_kv, n_tokens] (device, byte strides)
 // into dst rows [pos0, pos0 + n_tokens) of a [head_dim, n_head_kv, n_ctx]
 // cache with byte strides dst_s1 (head) and dst_s2 (position).

@@ -1,0 +1,266 @@
+// mul_mat.hip -- the step after attention on the device: MI_OP_QUANTIZE_Q8_0
+// (src/ops_cpu.cpp:462-479 -> src/quant.cpp:188-210) and MI_OP_MUL_MAT with
+// Q8_0 weights (src/ops_cpu.cpp:226-236), e.g. the attention output
+// projection. HBM-bound matrix-vector work: the weights are read once per
+// launch; a decode column reuses nothing else.
+//
+// Both reproduce the engine bit for bit:
+//  - activation blocks of 32: amax by a strict greater-than scan, d = amax /
+//    127 and id = 1 / d as correctly rounded float divisions, q = rint(x id)
+//    (round half to even, as lrintf) clamped to [-127, 127];
+//  - the dot product of a weight row and an activation column in the order
+//    of the reference's default (AVX2 + FMA) path: accumulator l (0..7) takes
+//    fma(float(int8 dot of bytes 4l..4l+3 of each block), fp16(w.d) * a.d,
+//    acc_l) block by block (v_dot4 gives that byte group's exact int32 sum),
+//    then ((acc0 + acc4) + (acc1 + acc5)) + ((acc2 + acc6) + (acc3 + acc7)).
+//    Lane l of an 8-lane group owns accumulator l; the horizontal sum is two
+//    xor exchanges (float addition is commutative, so each partial is the
+//    same value on both lanes that form it).
+#include <algorithm>
+
+#include "attn_common.h"
+#include "kernels.h"
+
+namespace mi {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// One thread per 32-element block of one activation row.
+__global__ void quantize_q8_0_act_kernel(const Q8Quantize p) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nb = p.ne0 / 32;
+  if (idx >= p.rows * nb) return;
+  const int64_t r = idx / nb, b = idx - r * nb;
+  const int64_t i1 = r % p.ne1, i2 = (r / p.ne1) % p.ne2, i3 = r / (p.ne1 * p.ne2);
+  const float* x = reinterpret_cast<const float*>(p.src + i1 * p.src_nb[1] + i2 * p.src_nb[2] +
+                                                  i3 * p.src_nb[3]) + 32 * b;
+  float v[32];
+#pragma unroll
+  for (int j = 0; j < 32; ++j) v[j] = gload<float>(x + j);  // rows are 4-byte aligned only
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const float av = fabsf(v[j]);
+    if (av > amax) amax = av;
+  }
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  char* y = p.dst + i1 * p.dst_nb[1] + i2 * p.dst_nb[2] + i3 * p.dst_nb[3] + 36 * b;
+  gstore<float>(y, d);
+#pragma unroll
+  for (int j = 0; j < 32; j += 4) {
+    unsigned word = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      int q = (int)__builtin_rintf(v[j + t] * id);
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+      word |= (unsigned)(q & 0xff) << (8 * t);
+    }
+    gstore<unsigned>(y + 4 + j, word);
+  }
+}
+
+// Rows of 8 lanes (32 rows per 256-thread workgroup); columns in chunks of
+// kQ8Cols, each lane keeping its accumulator for every column of the chunk.
+constexpr int kQ8Cols = 8;
+
+__global__ __launch_bounds__(256) void mul_mat_q8_0_kernel(const Q8MulMat p) {
+#pragma clang fp contract(off)
+  const int l = threadIdx.x & 7;
+  const int64_t row = (int64_t)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const bool live = row < p.n;  // dead lanes still join the exchanges
+  const char* w = p.w + (live ? row : 0) * p.w_nb1;
+  const int nblk = (int)(p.k / 32);
+  for (int64_t c0 = 0; c0 < p.m; c0 += kQ8Cols) {
+    const int nc = (int)min<int64_t>(kQ8Cols, p.m - c0);
+    float acc[kQ8Cols];
+#pragma unroll
+    for (int c = 0; c < kQ8Cols; ++c) acc[c] = 0.0f;
+    for (int b = 0; b < nblk; ++b) {
+      const char* wb = w + 34 * (int64_t)b;
+      // 34-byte blocks: the scale and the byte group are 2-byte aligned
+      const float wd = (float)__builtin_bit_cast(_Float16, gload<unsigned short>(wb));
+      const int wq = (int)((unsigned)gload<unsigned short>(wb + 2 + 4 * l) |
+                           ((unsigned)gload<unsigned short>(wb + 4 + 4 * l) << 16));
+#pragma unroll
+      for (int c = 0; c < kQ8Cols; ++c) {
+        if (c < nc) {
+          const char* ab = p.a + (c0 + c) * p.a_nb1 + 36 * (int64_t)b;
+          const float dxdy = wd * gload<float>(ab);
+          const int isum = __builtin_amdgcn_sdot4(wq, gload<int>(ab + 4 + 4 * l), 0, false);
+          acc[c] = __builtin_fmaf((float)isum, dxdy, acc[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kQ8Cols; ++c) {
+      if (c < nc) {
+        // lanes l and l^4 -> acc_l + acc_(l+4); then pairs; lane 0 holds
+        // ((acc0 + acc4) + (acc1 + acc5)) + ((acc2 + acc6) + (acc3 + acc7))
+        float s = acc[c] + __shfl_xor(acc[c], 4, 8);
+        s = s + __shfl_xor(s, 1, 8);
+        s = s + __shfl_xor(s, 2, 8);
+        if (live && l == 0)
+          gstore<float>(p.dst + row * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
+      }
+    }
+  }
+}
+
+// The streaming form, for weight rows of at most 1 KB (k <= 960: every matrix
+// of a 896-wide model), 16-byte aligned groups of 8 rows and M <= kQ8Cols
+// columns. One workgroup of 8 waves per CU; each wave walks row groups (8
+// rows) g = wave_id, wave_id + stride, ... through a ring of 2 LDS slots
+// filled by buffer_load ... lds (16 bytes per lane, one resource per group
+// bounded at the tensor's end, so bytes past it arrive as zeros without a
+// request, and a group past the end refills through a zero-sized resource).
+// Its 8-lane row groups read their byte groups back from the slot. Per
+// iteration a wave issues exactly M stores then 8 loads, so the wait for a
+// slot is the fixed vmcnt(M + 8) (vmcnt(8) the first time).
+constexpr int kQ8RowBytesMax = 1024;
+constexpr int kQ8RingWaves = 8;
+constexpr int kQ8Slot = 8 * kQ8RowBytesMax;
+constexpr int kQ8MaxBlocks = 30;                   // k <= 960
+constexpr int kQ8ActBytesMax = kQ8Cols * kQ8MaxBlocks * 36;
+constexpr int kQ8RingLds = kQ8RingWaves * 2 * kQ8Slot + kQ8ActBytesMax;
+
+template <int M>
+__global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel(const Q8MulMat p) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char ring_lds[];
+  lds_t* const lds = (lds_t*)ring_lds;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int nblk = (int)(p.k / 32);
+  const int abytes = nblk * 36;
+  char* const act_lds = ring_lds + kQ8RingWaves * 2 * kQ8Slot;
+  for (int i = threadIdx.x; i < M * abytes / 4; i += kQ8RingWaves * kWave) {
+    const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
+    *reinterpret_cast<unsigned*>(act_lds + c * abytes + o) = gload<unsigned>(p.a + c * p.a_nb1 + o);
+  }
+  const int64_t n_groups = (p.n + 7) / 8;
+  const int64_t stride = (int64_t)gridDim.x * kQ8RingWaves;
+  const int64_t g0 = (int64_t)blockIdx.x * kQ8RingWaves + wv;
+  const int64_t total = p.n * p.w_nb1;
+  const rsrc_t none = make_rsrc(p.w, 0u);
+  lds_t* const slots = lds + wv * 2 * kQ8Slot;
+  auto refill = [&](int s, int64_t g) __attribute__((always_inline)) {
+    rsrc_t r = none;
+    if (g < n_groups) {
+      const int64_t start = g * 8 * p.w_nb1;
+      r = make_rsrc(p.w + start, (unsigned)min<int64_t>(8 * p.w_nb1, total - start));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dma16(r, slots + s * kQ8Slot + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+  };
+  __syncthreads();  // the activation is staged (before the ring requests: the barrier waits for all loads)
+  refill(0, g0);
+  refill(1, g0 + stride);
+  const int l = lane & 7, rs = lane >> 3;
+  const lds_t* const act = lds + kQ8RingWaves * 2 * kQ8Slot;
+  // one column: this lane's activation byte groups and the block scales, in registers
+  float a_d[M == 1 ? kQ8MaxBlocks : 1];
+  int a_q[M == 1 ? kQ8MaxBlocks : 1];
+  if constexpr (M == 1) {
+#pragma unroll
+    for (int b = 0; b < kQ8MaxBlocks; ++b) {
+      a_d[b] = b < nblk ? lds_load<float>(act + 36 * b) : 0.f;
+      a_q[b] = b < nblk ? lds_load<int>(act + 36 * b + 4 + 4 * l) : 0;
+    }
+  }
+  int s = 0;
+  for (int64_t g = g0; g < n_groups; g += stride, s ^= 1) {
+    if (g == g0)
+      wait_vmem<8>();
+    else
+      wait_vmem<M + 8>();
+    const lds_t* const w = lds + (wv * 2 + s) * kQ8Slot + rs * (int)p.w_nb1;
+    float acc[M];
+#pragma unroll
+    for (int c = 0; c < M; ++c) acc[c] = 0.0f;
+    // blocks fully unrolled (k <= 960), used in order; the LDS reads of all
+    // of them can be issued ahead of the chain of multiply-adds
+#pragma unroll
+    for (int b = 0; b < kQ8MaxBlocks; ++b) {
+      const int bb = min(b, nblk - 1);  // reads stay in the row; blocks past it are not added
+      const lds_t* wb = w + 34 * bb;
+      const float wd = (float)__builtin_bit_cast(_Float16, lds_load<unsigned short>(wb));
+      const int wq = (int)((unsigned)lds_load<unsigned short>(wb + 2 + 4 * l) |
+                           ((unsigned)lds_load<unsigned short>(wb + 4 + 4 * l) << 16));
+#pragma unroll
+      for (int c = 0; c < M; ++c) {
+        const float dxdy = wd * (M == 1 ? a_d[b] : lds_load<float>(act + c * abytes + 36 * bb));
+        const int aq = M == 1 ? a_q[b] : lds_load<int>(act + c * abytes + 36 * bb + 4 + 4 * l);
+        const int isum = __builtin_amdgcn_sdot4(wq, aq, 0, false);
+        const float r = __builtin_fmaf((float)isum, dxdy, acc[c]);
+        acc[c] = b < nblk ? r : acc[c];
+      }
+    }
+    const int64_t row = g * 8 + rs;
+#pragma unroll
+    for (int c = 0; c < M; ++c) {
+      float t = acc[c] + __shfl_xor(acc[c], 4, 8);
+      t = t + __shfl_xor(t, 1, 8);
+      t = t + __shfl_xor(t, 2, 8);
+      acc[c] = t;
+    }
+    // the slot's reads are done before it is refilled; then M stores (row 0
+    // of a group always exists, so every store instruction issues), 8 loads
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int c = 0; c < M; ++c)
+      if (row < p.n && l == 0) gstore<float>(p.dst + row * p.dst_nb0 + c * p.dst_nb1, acc[c]);
+    refill(s, g + 2 * stride);
+  }
+  wait_vmem<0>();
+}
+
+hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream) {
+  const int64_t n = p.rows * (p.ne0 / 32);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize_q8_0_act_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) {
+  if (p.n == 0 || p.m == 0) return hipSuccess;
+  const bool rows_form = p.w_nb1 <= kQ8RowBytesMax && p.k <= 960 && p.m <= kQ8Cols &&
+                         (8 * p.w_nb1) % 16 == 0 && reinterpret_cast<uintptr_t>(p.w) % 16 == 0 &&
+                         p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0 &&
+                         p.n * p.w_nb1 < (int64_t)1 << 40;
+  if (rows_form) {
+    static const hipError_t attr = [] {
+      hipError_t e = hipSuccess;
+      const void* fns[kQ8Cols] = {
+          (const void*)&mul_mat_q8_0_ring_kernel<1>, (const void*)&mul_mat_q8_0_ring_kernel<2>,
+          (const void*)&mul_mat_q8_0_ring_kernel<3>, (const void*)&mul_mat_q8_0_ring_kernel<4>,
+          (const void*)&mul_mat_q8_0_ring_kernel<5>, (const void*)&mul_mat_q8_0_ring_kernel<6>,
+          (const void*)&mul_mat_q8_0_ring_kernel<7>, (const void*)&mul_mat_q8_0_ring_kernel<8>};
+      for (const void* f : fns)
+        if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8RingLds);
+      return e;
+    }();
+    if (attr != hipSuccess) return attr;
+    const int64_t groups = (p.n + 7) / 8;
+    const unsigned grid = (unsigned)std::min<int64_t>(n_cu > 0 ? n_cu : 256, (groups + kQ8RingWaves - 1) / kQ8RingWaves);
+    const dim3 bs(kQ8RingWaves * kWave);
+    switch (p.m) {
+      case 1: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<1>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      case 2: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<2>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      case 3: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<3>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      case 4: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<4>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      case 5: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<5>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      case 6: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<6>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      case 7: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<7>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+      default: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<8>, dim3(grid), bs, kQ8RingLds, stream, p); break;
+    }
+  } else {
+    hipLaunchKernelGGL(mul_mat_q8_0_kernel, dim3((unsigned)((p.n + 31) / 32)), dim3(256), 0, stream,
+                       p);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace mi

@@ -940,6 +940,70 @@ int mi_hip_rope_append(const mi_hip_rope_args* a) {
   return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "rope append launch");
 }
 
+int mi_hip_op_quantize_q8_0(mi_tensor* dst, void* stream) {
+  if (!dst || dst->op != MI_OP_QUANTIZE_Q8_0)
+    return fail(MI_HIP_E_INVALID, "dst is not a QUANTIZE_Q8_0 node");
+  const mi_tensor* s = dst->src[0];
+  int rc;
+  if ((rc = check_f32(s, "src"))) return rc;
+  if (!dst->data) return fail(MI_HIP_E_INVALID, "dst: missing data");
+  if (dst->type != MI_TYPE_Q8_0_ACT) return fail(MI_HIP_E_UNSUPPORTED, "dst must be Q8_0_ACT");
+  for (int i = 0; i < 4; ++i)
+    if (dst->ne[i] != s->ne[i]) return fail(MI_HIP_E_INVALID, "QUANTIZE_Q8_0 shape differs from its source");
+  if (s->ne[0] % 32) return fail(MI_HIP_E_INVALID, "ne[0] = %lld is not a multiple of 32", (long long)s->ne[0]);
+  if (s->nb[0] != 4) return fail(MI_HIP_E_UNSUPPORTED, "src rows must be contiguous (nb[0] = 4)");
+  for (int i = 1; i < 4; ++i)
+    if (s->nb[i] % 4 || dst->nb[i] % 4)
+      return fail(MI_HIP_E_INVALID, "QUANTIZE_Q8_0 strides must be multiples of 4 bytes");
+  mi::Q8Quantize p{};
+  p.src = static_cast<const char*>(s->data);
+  p.dst = static_cast<char*>(dst->data);
+  for (int i = 0; i < 4; ++i) {
+    p.src_nb[i] = (int64_t)s->nb[i];
+    p.dst_nb[i] = (int64_t)dst->nb[i];
+  }
+  p.ne0 = s->ne[0];
+  p.ne1 = s->ne[1];
+  p.ne2 = s->ne[2];
+  p.rows = s->ne[1] * s->ne[2] * s->ne[3];
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_quantize_q8_0_act(p, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "quantize launch");
+}
+
+int mi_hip_op_mul_mat(mi_tensor* dst, void* stream) {
+  if (!dst || dst->op != MI_OP_MUL_MAT) return fail(MI_HIP_E_INVALID, "dst is not a MUL_MAT node");
+  const mi_tensor* a = dst->src[0];
+  const mi_tensor* b = dst->src[1];
+  int rc;
+  if ((rc = check_f32(dst, "dst"))) return rc;
+  if (!a || !a->data || !b || !b->data) return fail(MI_HIP_E_INVALID, "MUL_MAT: missing operand");
+  if (a->type != MI_TYPE_Q8_0) return fail(MI_HIP_E_UNSUPPORTED, "MUL_MAT: only Q8_0 weights (type %d)", (int)a->type);
+  if (b->type != MI_TYPE_Q8_0_ACT)
+    return fail(MI_HIP_E_INVALID, "MUL_MAT: src[1] must be the Q8_0_ACT output of QUANTIZE_Q8_0");
+  const int64_t k = a->ne[0], n = a->ne[1], m = b->ne[1];
+  if (k % 32 || b->ne[0] != k) return fail(MI_HIP_E_INVALID, "MUL_MAT: k = %lld must match and be a multiple of 32", (long long)k);
+  if (dst->ne[0] != n || dst->ne[1] != m || a->ne[2] * a->ne[3] != 1 || b->ne[2] * b->ne[3] != 1)
+    return fail(MI_HIP_E_INVALID, "MUL_MAT shapes are inconsistent");
+  if (a->nb[1] % 2 || a->nb[1] < (size_t)(k / 32 * 34) || b->nb[1] % 4 || b->nb[1] < (size_t)(k / 32 * 36) ||
+      dst->nb[0] % 4 || dst->nb[1] % 4)
+    return fail(MI_HIP_E_INVALID, "MUL_MAT strides do not fit the block layouts");
+  mi::Q8MulMat p{};
+  p.w = static_cast<const char*>(a->data);
+  p.a = static_cast<const char*>(b->data);
+  p.dst = static_cast<char*>(dst->data);
+  p.w_nb1 = (int64_t)a->nb[1];
+  p.a_nb1 = (int64_t)b->nb[1];
+  p.dst_nb0 = (int64_t)dst->nb[0];
+  p.dst_nb1 = (int64_t)dst->nb[1];
+  p.k = k;
+  p.n = n;
+  p.m = m;
+  if ((rc = bind_device())) return rc;
+  hipError_t e = mi::launch_mul_mat_q8_0(p, g.n_cu, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "mul_mat launch");
+}
+
 int mi_hip_op_attn_kqv(mi_tensor* dst, void* stream) {
   if (!dst || dst->op != MI_OP_ATTN_KQV) return fail(MI_HIP_E_INVALID, "dst is not an ATTN_KQV node");
   const mi_tensor* pr = dst->src[0];

@@ -13,11 +13,15 @@ LIB_PATH = os.path.join(HERE, "libmi_hip_attn.so")
 
 MI_TYPE_F32 = 0
 MI_TYPE_F16 = 1
+MI_TYPE_Q8_0 = 2
+MI_TYPE_Q8_0_ACT = 4
 
 MI_OP_NONE = 0
+MI_OP_MUL_MAT = 5
 MI_OP_ROPE = 6
 MI_OP_SOFTMAX = 7
 MI_OP_CPY = 10
+MI_OP_QUANTIZE_Q8_0 = 11
 MI_OP_VIEW = 13
 MI_OP_ATTN_QK = 16
 MI_OP_ATTN_KQV = 17
@@ -146,6 +150,8 @@ SIGNATURES = {
     "mi_hip_op_attn_kqv": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_op_attn_fused": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_op_rope": ([ctypes.POINTER(MiTensor), _P], _I),
+    "mi_hip_op_quantize_q8_0": ([ctypes.POINTER(MiTensor), _P], _I),
+    "mi_hip_op_mul_mat": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_rope_append": ([ctypes.POINTER(RopeArgs)], _I),
     "mi_hip_graph_prepare": ([ctypes.POINTER(MiCgraph)], _I),
     "mi_hip_compute_forward": ([ctypes.POINTER(MiTensor), _I, _I], _I),

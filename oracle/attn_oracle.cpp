@@ -15,6 +15,11 @@
 //   MI_OP_ATTN_KQV      src/ops_cpu.cpp:386-410
 //   MI_OP_ROPE          src/ops_cpu.cpp:270-302 (NEOX halves; op_params of
 //                       src/graph.cpp:146-154)
+//   MI_OP_QUANTIZE_Q8_0 src/ops_cpu.cpp:462-479 with src/quant.cpp:188-210
+//   MI_OP_MUL_MAT, Q8_0 weights: src/ops_cpu.cpp:226-236 with the dot product
+//                       the reference dispatches to on AVX2 hosts
+//                       (src/quant.cpp:240-247 -> src/quant_avx2.cpp:174-185,
+//                       block dot :97-105, horizontal sum :74-83)
 //   F16 -> F32          src/quant.cpp:26-63 (IEEE binary16 widening)
 // Build flags: -O3 -ffp-contract=off, no -ffast-math, no -march: the same
 // scalar float semantics as the reference's baseline x86-64 build.
@@ -336,6 +341,100 @@ float oracle_fp16_to_fp32(uint16_t h) {
 
 void oracle_fp16_to_fp32_row(const uint16_t* src, float* dst, int64_t n) {
   for (int64_t i = 0; i < n; ++i) dst[i] = oracle_fp16_to_fp32(src[i]);
+}
+
+// ---- Q8_0 ------------------------------------------------------------------
+// Weight block: fp16 scale then 32 int8 (34 bytes, src/quant.h:22-28).
+// Activation block: float scale then 32 int8 (36 bytes, src/quant.h:122-127).
+#pragma pack(push, 1)
+struct OracleBlockQ8 {
+  uint16_t d;
+  int8_t qs[32];
+};
+#pragma pack(pop)
+struct OracleBlockAct {
+  float d;
+  int8_t qs[32];
+};
+static_assert(sizeof(OracleBlockQ8) == 34 && sizeof(OracleBlockAct) == 36, "Q8_0 block layouts");
+
+// One row of n floats -> n/32 activation blocks: amax of the block (strict
+// greater-than scan), d = amax / 127, id = 1 / d (0 for an all-zero block),
+// q = lrintf(x * id) clamped to [-127, 127].
+void oracle_quantize_row_q8_0_act(const float* x, OracleBlockAct* y, int64_t n) {
+  for (int64_t i = 0; i < n / 32; ++i) {
+    const float* xb = x + i * 32;
+    float amax = 0.0f;
+    for (int j = 0; j < 32; ++j) {
+      const float av = std::fabs(xb[j]);
+      if (av > amax) amax = av;
+    }
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    y[i].d = d;
+    for (int j = 0; j < 32; ++j) {
+      int32_t q = (int32_t)lrintf(xb[j] * id);
+      if (q > 127) q = 127;
+      if (q < -127) q = -127;
+      y[i].qs[j] = (int8_t)q;
+    }
+  }
+}
+
+// Weight row . activation row over n elements, in the order of the
+// reference's default (AVX2 + FMA) dot product: eight float accumulators,
+// accumulator l takes fma(float(sum of the block's int8 products 4l..4l+3),
+// fp16(w.d) * a.d, acc[l]) block by block, then the horizontal sum
+// ((acc0 + acc4) + (acc1 + acc5)) + ((acc2 + acc6) + (acc3 + acc7)).
+float oracle_vec_dot_q8_0_act(const OracleBlockQ8* w, const OracleBlockAct* a, int64_t n) {
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t i = 0; i < n / 32; ++i) {
+    const float dxdy = oracle_fp16_to_fp32(w[i].d) * a[i].d;
+    for (int l = 0; l < 8; ++l) {
+      int32_t isum = 0;
+      for (int k = 0; k < 4; ++k) isum += (int32_t)w[i].qs[4 * l + k] * (int32_t)a[i].qs[4 * l + k];
+      acc[l] = std::fma((float)isum, dxdy, acc[l]);
+    }
+  }
+  float s[4];
+  for (int k = 0; k < 4; ++k) s[k] = acc[k] + acc[k + 4];
+  return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+// MI_OP_MUL_MAT with Q8_0 weights a [k, n] (row i at a->nb[1] i) and a
+// Q8_0_ACT activation b [k, m] (column j at b->nb[1] j): dst(i, j) =
+// vec_dot(row i, column j); rows split over threads (each row's order is the
+// same whichever thread computes it).
+void oracle_mul_mat_q8_0(mi_tensor* dst, int ith, int nth) {
+  const mi_tensor* a = dst->src[0];
+  const mi_tensor* b = dst->src[1];
+  const int64_t k = a->ne[0], n = a->ne[1], m = b->ne[1];
+  int64_t lo, hi;
+  share_of(n, ith, nth, &lo, &hi);
+  for (int64_t i = lo; i < hi; ++i) {
+    const auto* arow = reinterpret_cast<const OracleBlockQ8*>(static_cast<const char*>(a->data) +
+                                                             i * (int64_t)a->nb[1]);
+    for (int64_t j = 0; j < m; ++j) {
+      const auto* brow = reinterpret_cast<const OracleBlockAct*>(
+          static_cast<const char*>(b->data) + j * (int64_t)b->nb[1]);
+      elem(dst, i, j, 0) = oracle_vec_dot_q8_0_act(arow, brow, k);
+    }
+  }
+}
+
+// Contiguous forms: x [m][k] floats -> act [m][k/32] blocks; W [n][k/32]
+// blocks . act -> dst [m][n] (dst(i, j) at j * n + i, the engine's [n, m]).
+void oracle_quantize_q8_0_act(const float* x, void* act, int64_t k, int64_t m) {
+  for (int64_t j = 0; j < m; ++j)
+    oracle_quantize_row_q8_0_act(x + j * k, static_cast<OracleBlockAct*>(act) + j * (k / 32), k);
+}
+
+void oracle_mul_mat_q8_0_contig(const void* w, const void* act, float* dst, int64_t k, int64_t n,
+                                int64_t m) {
+  for (int64_t j = 0; j < m; ++j)
+    for (int64_t i = 0; i < n; ++i)
+      dst[j * n + i] = oracle_vec_dot_q8_0_act(static_cast<const OracleBlockQ8*>(w) + i * (k / 32),
+                                               static_cast<const OracleBlockAct*>(act) + j * (k / 32), k);
 }
 
 // Runs ATTN_QK -> SOFTMAX -> ATTN_KQV on contiguous buffers:

@@ -121,6 +121,25 @@ class Oracle(CpuAttention):
         fn(x.ctypes.data, y.ctypes.data, d, h, t, n_past, n_dims, ctypes.c_float(freq_base))
         return y
 
+    def quantize_q8_0_act(self, x):
+        """Activation rows x (m, k) -> raw Q8_0_ACT blocks (m * k/32 * 36 bytes)."""
+        x = np.ascontiguousarray(x, np.float32)
+        m, k = x.shape
+        out = np.empty(m * (k // 32) * 36, np.uint8)
+        fn = self.lib.oracle_quantize_q8_0_act
+        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64]
+        fn(x.ctypes.data, out.ctypes.data, k, m)
+        return out
+
+    def mul_mat_q8_0(self, w, act, k, n, m):
+        """Raw Q8_0 weight rows (n x k/32 blocks) . raw activation blocks -> (m, n)."""
+        dst = np.empty((m, n), np.float32)
+        fn = self.lib.oracle_mul_mat_q8_0_contig
+        fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3
+        fn(np.ascontiguousarray(w).ctypes.data, np.ascontiguousarray(act).ctypes.data,
+           dst.ctypes.data, k, n, m)
+        return dst
+
     def split_range(self, n, ith, nth):
         lo, hi = ctypes.c_int64(), ctypes.c_int64()
         self.lib.oracle_split_range(n, ith, nth, ctypes.byref(lo), ctypes.byref(hi))
@@ -161,3 +180,17 @@ def _fp16_lut():
         fn(codes.ctypes.data, lut.ctypes.data, 65536)
         _cache["lut"] = lut
     return _cache["lut"]
+
+
+def q8_weight_blocks(w_raw, n, k):
+    """Raw Q8_0 weight rows -> (fp16 scales (n, k/32), int8 values (n, k/32, 32))."""
+    b = np.ascontiguousarray(w_raw).view(np.uint8).reshape(n, k // 32, 34)
+    d = b[:, :, :2].copy().view(np.float16)[:, :, 0]
+    return d, b[:, :, 2:].copy().view(np.int8)
+
+
+def q8_act_blocks(a_raw, m, k):
+    """Raw Q8_0_ACT rows -> (float scales (m, k/32), int8 values (m, k/32, 32))."""
+    b = np.ascontiguousarray(a_raw).view(np.uint8).reshape(m, k // 32, 36)
+    d = b[:, :, :4].copy().view(np.float32)[:, :, 0]
+    return d, b[:, :, 4:].copy().view(np.int8)

@@ -122,6 +122,27 @@ int ref_rope(const float* src, float* dst, int head_dim, int n_head, int n_token
 
 float ref_fp16_to_fp32(uint16_t h) { return mi_fp16_to_fp32(h); }
 
+// The reference's Q8_0 routines on contiguous buffers: weight rows from
+// floats (src/quant.cpp:129-153), activation rows (src/quant.cpp:188-210), and
+// the dot product mul_mat calls (src/quant.cpp:240-247, its runtime dispatch
+// included) for every (row i, column j): dst[j * n + i].
+void ref_quantize_rows_q8_0(const float* x, void* w, int64_t k, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    mi_quantize_row_q8_0(x + i * k, static_cast<block_q8_0*>(w) + i * (k / MI_QK8_0), k);
+}
+
+void ref_quantize_rows_q8_0_act(const float* x, void* act, int64_t k, int64_t m) {
+  for (int64_t j = 0; j < m; ++j)
+    mi_quantize_row_q8_0_act(x + j * k, static_cast<block_q8_0_act*>(act) + j * (k / MI_QK8_0), k);
+}
+
+void ref_mul_mat_q8_0(const void* w, const void* act, float* dst, int64_t k, int64_t n, int64_t m) {
+  for (int64_t j = 0; j < m; ++j)
+    for (int64_t i = 0; i < n; ++i)
+      dst[j * n + i] = mi_vec_dot_q8_0_wact(static_cast<const block_q8_0*>(w) + i * (k / MI_QK8_0),
+                                            static_cast<const block_q8_0_act*>(act) + j * (k / MI_QK8_0), k);
+}
+
 // The reference's own struct layout (src/tensor.h:122-160, src/graph.h:19-47),
 // in the order of mi_hip_abi_layout.
 int ref_abi_layout(size_t* out, int n) {

@@ -67,6 +67,18 @@ ROPE_CASES = {
 }
 
 
+# name: (k, n rows, m columns) of MI_OP_MUL_MAT with Q8_0 weights
+Q8_CASES = {
+    "q8_kat": (64, 5, 4),
+    "q8_oproj_rows": (896, 64, 3),    # Qwen2.5-0.5B attn_output k, 64 of its 896 rows
+    "q8_ffn_down_rows": (4864, 24, 2),  # ffn_down k = 4864
+}
+
+
+def x_ptr(a):
+    return a.ctypes.data
+
+
 def f16_lut(ref):
     import ctypes
     fn = ref.lib.ref_fp16_to_fp32_row
@@ -134,6 +146,35 @@ def main():
                                   "n_dims": n_dims, "freq_base": base,
                                   "sha256_src": sha256(x), "sha256_dst": sha256(y)}
         print(f"{name}: {x.shape}")
+
+    # Q8_0 (src/quant.cpp): weight rows from seeded N(0, 0.02) floats, the
+    # activation quantized by the reference, and mul_mat's dot products as the
+    # reference dispatches them. Row/column counts kept small (fixtures).
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    ref.lib.ref_quantize_rows_q8_0.argtypes = [vp, vp, i64, i64]
+    ref.lib.ref_quantize_rows_q8_0_act.argtypes = [vp, vp, i64, i64]
+    ref.lib.ref_mul_mat_q8_0.argtypes = [vp, vp, vp, i64, i64, i64]
+    manifest["q8_0"] = {}
+    rng = np.random.default_rng(8080)
+    for name, (k, n, m) in Q8_CASES.items():
+        wf = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        if name == "q8_kat":
+            x[0, :32] = 0.0                                   # all-zero block: d = 0, q = 0
+            x[1, :32] = np.arange(32, dtype=np.float32) - 15.5  # ties at .5 (amax 15.5)
+            x[1, 31] = 127.0                                   # amax 127 -> d = 1, ties stay ties
+            x[2, 32:64] = -x[2, 32:64]
+        w = np.empty(n * (k // 32) * 34, np.uint8)
+        ref.lib.ref_quantize_rows_q8_0(x_ptr(wf), w.ctypes.data, k, n)
+        act = np.empty(m * (k // 32) * 36, np.uint8)
+        ref.lib.ref_quantize_rows_q8_0_act(x_ptr(x), act.ctypes.data, k, m)
+        dst = np.empty((m, n), np.float32)
+        ref.lib.ref_mul_mat_q8_0(w.ctypes.data, act.ctypes.data, dst.ctypes.data, k, n, m)
+        np.savez(os.path.join(OUT_DIR, name + ".npz"), w=w, x=x, act=act, dst=dst)
+        manifest["q8_0"][name] = {"k": k, "n": n, "m": m, "sha256_w": sha256(w),
+                                  "sha256_x": sha256(x), "sha256_act": sha256(act),
+                                  "sha256_dst": sha256(dst)}
+        print(f"{name}: k={k} n={n} m={m}")
 
     # The reference's F16 widening over every code, as float32 bit patterns.
     if lut is None:

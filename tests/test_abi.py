@@ -116,6 +116,33 @@ def test_status_and_errors_without_device(lib):
     assert lib.mi_hip_rope_append(None) == 1
     ra = mh.RopeArgs()
     assert lib.mi_hip_rope_append(ctypes.byref(ra)) == 1 and "NULL" in lib.last_error()
+    # Q8_0: wrong nodes, F32 weights, k not a multiple of 32, unsplit rows
+    t.op = mh.MI_OP_SOFTMAX
+    assert lib.mi_hip_op_quantize_q8_0(ctypes.byref(t), None) == 1
+    assert lib.mi_hip_op_mul_mat(ctypes.byref(t), None) == 1
+    f32 = np.zeros(4096, np.float32)
+    x = mh.make_tensor(f32.ctypes.data, [64, 2], [4, 256])
+    q = mh.make_tensor(f32.ctypes.data, [64, 2], [36, 72], type_=mh.MI_TYPE_Q8_0_ACT,
+                       op=mh.MI_OP_QUANTIZE_Q8_0, src=[x])
+    x48 = mh.make_tensor(f32.ctypes.data, [48, 2], [4, 192])
+    q48 = mh.make_tensor(f32.ctypes.data, [48, 2], [36, 72], type_=mh.MI_TYPE_Q8_0_ACT,
+                         op=mh.MI_OP_QUANTIZE_Q8_0, src=[x48])
+    assert lib.mi_hip_op_quantize_q8_0(ctypes.byref(q48), None) == 1  # 48 % 32
+    xs = mh.make_tensor(f32.ctypes.data, [64, 2], [8, 512])
+    qs = mh.make_tensor(f32.ctypes.data, [64, 2], [36, 72], type_=mh.MI_TYPE_Q8_0_ACT,
+                        op=mh.MI_OP_QUANTIZE_Q8_0, src=[xs])
+    assert lib.mi_hip_op_quantize_q8_0(ctypes.byref(qs), None) == 5  # nb[0] != 4
+    wf = mh.make_tensor(f32.ctypes.data, [64, 3], [4, 256])  # F32 weights
+    d = mh.make_tensor(f32.ctypes.data, [3, 2], [4, 12], op=mh.MI_OP_MUL_MAT, src=[wf, q])
+    assert lib.mi_hip_op_mul_mat(ctypes.byref(d), None) == 5 and "Q8_0" in lib.last_error()
+    wq = mh.make_tensor(f32.ctypes.data, [64, 3], [34, 68], type_=mh.MI_TYPE_Q8_0)
+    d = mh.make_tensor(f32.ctypes.data, [3, 2], [4, 12], op=mh.MI_OP_MUL_MAT, src=[wq, x])
+    assert lib.mi_hip_op_mul_mat(ctypes.byref(d), None) == 1  # activation not quantized
+    d = mh.make_tensor(f32.ctypes.data, [4, 2], [4, 16], op=mh.MI_OP_MUL_MAT, src=[wq, q])
+    assert lib.mi_hip_op_mul_mat(ctypes.byref(d), None) == 1  # dst rows != weight rows
+    wq = mh.make_tensor(f32.ctypes.data, [64, 3], [34, 66], type_=mh.MI_TYPE_Q8_0)
+    d = mh.make_tensor(f32.ctypes.data, [3, 2], [4, 12], op=mh.MI_OP_MUL_MAT, src=[wq, q])
+    assert lib.mi_hip_op_mul_mat(ctypes.byref(d), None) == 1  # row stride below 2 blocks
     # A node that is not attention and not a KV write is not ours.
     t.op = 4  # ADD
     assert lib.mi_hip_compute_forward(ctypes.byref(t), 0, 1) == 0

@@ -280,3 +280,53 @@ def test_rope_oracle_equals_reference_library(oracle):
         want = np.empty_like(x)
         fn(x.ctypes.data, want.ctypes.data, d, h, t, n_past, n_dims, ctypes.c_float(base))
         assert np.array_equal(bits(oracle.rope(x, n_past, n_dims, base)), bits(want))
+
+
+# ---- Q8_0: MI_OP_QUANTIZE_Q8_0 and MI_OP_MUL_MAT with Q8_0 weights -----------
+
+def test_q8_0_matches_reference_goldens_bitwise(oracle, golden_manifest):
+    for name, c in golden_manifest["q8_0"].items():
+        g = load_golden(name)
+        for key in ("w", "x", "act", "dst"):
+            assert cpu_attention.sha256(g[key]) == c["sha256_" + key], (name, key)
+        act = oracle.quantize_q8_0_act(g["x"])
+        assert np.array_equal(act, g["act"]), name
+        dst = oracle.mul_mat_q8_0(g["w"], g["act"], c["k"], c["n"], c["m"])
+        assert np.array_equal(bits(dst), bits(g["dst"])), name
+
+
+def test_q8_0_activation_known_answers(oracle):
+    # all-zero block -> scale 0, values 0; amax 127 -> scale exactly 1, and
+    # x.5 values round half to even (lrintf); |q| never passes 127
+    x = np.zeros((1, 64), np.float32)
+    x[0, 32:] = np.arange(32, dtype=np.float32) - 15.5
+    x[0, 63] = 127.0
+    d, q = cpu_attention.q8_act_blocks(oracle.quantize_q8_0_act(x), 1, 64)
+    assert d[0, 0] == 0 and not q[0, 0].any()
+    assert d[0, 1] == np.float32(1.0)
+    want = np.rint(x[0, 32:]).astype(np.int64)  # numpy rint: half to even
+    want[-1] = 127
+    assert np.array_equal(q[0, 1].astype(np.int64), want)
+    y = np.random.default_rng(9).standard_normal((3, 96)).astype(np.float32) * 50
+    d, q = cpu_attention.q8_act_blocks(oracle.quantize_q8_0_act(y), 3, 96)
+    amax = np.abs(y.reshape(3, 3, 32)).max(axis=2)
+    assert np.array_equal(d, (amax / np.float32(127)).astype(np.float32))
+    assert np.abs(q).max() == 127 and np.all(np.abs(q.astype(np.int64)) <= 127)
+
+
+def test_q8_0_dot_equals_dequantized_float64_product(oracle, golden_manifest):
+    # The order-free value of the dot: sum over blocks of fp16(w.d) * a.d *
+    # sum(w.qs * a.qs), in float64. A dropped scale, swapped operand or wrong
+    # grouping moves the result far beyond float rounding.
+    for name in golden_manifest["q8_0"]:
+        c = golden_manifest["q8_0"][name]
+        g = load_golden(name)
+        k, n, m = c["k"], c["n"], c["m"]
+        wd, wq = cpu_attention.q8_weight_blocks(g["w"], n, k)
+        ad, aq = cpu_attention.q8_act_blocks(g["act"], m, k)
+        isum = np.einsum("nbk,mbk->mnb", wq.astype(np.int64), aq.astype(np.int64))
+        want = np.einsum("mnb,nb,mb->mn", isum.astype(np.float64), wd.astype(np.float64),
+                         ad.astype(np.float64))
+        got = oracle.mul_mat_q8_0(g["w"], g["act"], k, n, m)
+        scale = np.abs(want).max() + 1e-12
+        assert np.abs(got - want).max() <= 1e-5 * scale, name
