@@ -13,6 +13,7 @@ constexpr int kWave = 64;
 // Decode (one query token against n_kv cached positions).
 // ---------------------------------------------------------------------------
 constexpr int kDecodeMaxItems = 32;  // items per launch (they ride in kernarg)
+constexpr int kDecodeEarlyMax = 8;   // largest group merged by its first finisher
 constexpr int kDecodeSub = 16;       // positions per sub-tile (one wave's unit of work)
 constexpr int kDecodeWaves = 4;      // waves per workgroup (one per SIMD)
 
@@ -46,6 +47,8 @@ struct DecodeParams {
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
   int32_t n_wg;         // workgroups
   int32_t cst;          // arrival counters per group: 1 + teams of its largest item
+  int32_t early;        // groups of 2..kDecodeEarlyMax workgroups merged by their first finisher
+  uint32_t epoch;       // launch stamp of early records (nonzero, new for every launch)
   float scale_log2e;    // softmax scale * log2(e)
   float* rec;           // one record per workgroup
   unsigned* cnt;        // cst arrival counters per (item, group); zero between launches

@@ -44,6 +44,16 @@
 // before the workgroup barrier that precedes the counter increment, and the
 // reader issues its loads only after the increment returned. (A device-scope
 // fence would write back and invalidate the XCD's whole L2 instead.)
+//
+// Early combining, for groups of 2..kDecodeEarlyMax workgroups when every
+// workgroup of the launch is resident at once (the host sets p.early): the
+// group's first workgroup to finish claims the merge with one atomic (issued
+// while its waves deposit); the others store their record as 64-bit (value,
+// launch epoch) words and exit, with no acknowledgement wait and no counter.
+// The merger polls the records until every word carries this launch's epoch
+// and merges all parts in part order. Its wait overlaps the other parts'
+// streaming, so after the last part finishes only that part's stores, one
+// poll and the merge remain.
 #include <cstdlib>
 #include <type_traits>
 
@@ -197,7 +207,11 @@ struct DecodeCfg {
   static constexpr int NB = NB0 > 4 ? 4 : NB0;    // ring depth per wave
   static constexpr int HSL = 4 * HS;              // head slots (G <= HSL)
   static constexpr int DEPF = HSL * (D + 2);      // floats of one wave's deposit
-  static constexpr int REC = (DEPF + 3) & ~3;     // floats per record
+  // A record: DEPF floats (team protocol) or DEPF 64-bit (value, epoch) words
+  // (early protocol); every workgroup's record slot holds the larger.
+  static constexpr int REC = 2 * DEPF;            // 4-byte units per record slot
+  static constexpr int NP = HSL * D / 4;          // merge: (head slot, float4) pairs
+  static constexpr int NSUB = NWV * kWave / NP;   // merge: record subsets
   static constexpr int NE = D / 64;               // float4 column blocks per lane
   // LDS layout (bytes). A wave's deposit overlays its own ring once the
   // wave's last loads have landed.
@@ -211,6 +225,12 @@ struct DecodeCfg {
   static_assert(SUBB % 1024 == 0, "1 KB load granularity");
   static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
   static_assert(DEPF * 4 <= NB * SLOTB, "a deposit fits its wave's ring");
+  // After the loop: an early merger's own partial behind wave 0's deposit;
+  // the merges' exchange area from wave 1's ring on.
+  static constexpr int L_OWN = L_RING + ((DEPF * 4 + 15) & ~15);
+  static constexpr int L_TMP = L_RING + NB * SLOTB;
+  static_assert(L_OWN + NP * 24 <= L_RING + NB * SLOTB, "own partial in wave 0's ring");
+  static_assert(NSUB <= 1 || L_TMP + NSUB * NP * 24 <= L_RING + NWV * NB * SLOTB, "merge exchange");
   // vmcnt allowed while waiting for a slot's K (its V and the later slots may
   // still be in flight) and for its V.
   static constexpr int WAIT_K = NDK + NDMA * (NB - 1);
@@ -475,6 +495,18 @@ void decode_kernel(const DecodeParams p) {
   // The waves meet in LDS: wave w's deposit at the start of its ring, once
   // its last loads (including the zero-filling ones past the share) landed.
   wait_vmem<0>();
+  // Early protocol (groups of 2..kDecodeEarlyMax workgroups, every workgroup
+  // of the launch resident): the group's first workgroup to get here merges,
+  // the others only store stamped records. The claim's round trip overlaps
+  // the deposits.
+  unsigned* const gcnt = p.cnt + (int64_t)gid * p.cst;
+  unsigned* const flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
+  const bool early = p.early && kpg > 1 && kpg <= kDecodeEarlyMax;
+  // (As asm, so that the compiler's wait before the deposits' LDS writes does
+  // not wait for it: the result is waited for explicitly below.)
+  unsigned claim = 1u;
+  if (early && threadIdx.x == 0)
+    asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(claim) : "v"(gcnt), "v"(1u) : "memory");
   auto dep_at = [&](int w) { return reinterpret_cast<float*>(lds_dyn + C::L_RING + w * NB * C::SLOTB); };
 #pragma unroll
   for (int h = 0; h < HS; ++h) l[h] = row_sum16(l[h]);
@@ -492,7 +524,115 @@ void decode_kernel(const DecodeParams p) {
       }
     }
   }
+  if (early && threadIdx.x == 0) {
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(claim) : : "memory");
+    flag[0] = claim == 0u;
+  }
   wg_barrier();
+  const bool merger = early && __builtin_amdgcn_readfirstlane(flag[0]) != 0;
+  unsigned long long* const recw = reinterpret_cast<unsigned long long*>(p.rec);
+  const unsigned long long ep = (unsigned long long)p.epoch << 32;
+  float* const own = reinterpret_cast<float*>(lds_dyn + C::L_OWN);
+
+  // The early merger: every part's partial in part order (its own from LDS,
+  // the others' stamped records polled until their words carry this launch's
+  // epoch; the other parts started before this workgroup finished and all of
+  // the launch's workgroups are resident, so they complete; a bounded poll
+  // count still ends the wait, with NaN output), subsets combined in order,
+  // O written, the claim counter re-armed (every other part claimed before it
+  // stored, so no increment is still in flight).
+  auto merge_early = [&]() __attribute__((always_inline)) {
+    constexpr int NP = C::NP, NSUB = C::NSUB;
+    constexpr int RB = (kDecodeEarlyMax + NSUB - 1) / NSUB;  // parts per subset
+    constexpr int kMaxPolls = 1 << 22;
+    constexpr unsigned long long kHi = 0xffffffff00000000ull;
+    wg_barrier();  // the own partial is in LDS
+    const int tt = threadIdx.x;
+    const int pair = tt % NP, sub = tt / NP;
+    const int hs = pair / (D / 4), cq = pair % (D / 4);
+    float mx = -INFINITY, lt = 0.f;
+    f32x4 at = {0.f, 0.f, 0.f, 0.f};
+    bool lost = false;
+    if (sub < NSUB) {
+      const unsigned long long* const g0 = recw + (int64_t)(wg - part) * (C::REC / 2) + hs * (D + 2);
+      auto word = [&](int i, int k) __attribute__((always_inline)) {
+        return g0 + (int64_t)min(sub + i * NSUB, kpg - 1) * (C::REC / 2) +
+               (k < 4 ? 4 * cq + k : D + (k - 4));
+      };
+      auto polled = [&](int i) { return sub + i * NSUB < kpg && sub + i * NSUB != part; };
+      unsigned long long w[RB][6];
+#pragma unroll
+      for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int k = 0; k < 6; ++k)
+          w[i][k] = polled(i) ? __hip_atomic_load(word(i, k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ep;
+      for (int n = 0;; ++n) {
+        bool fresh = true;
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int k = 0; k < 6; ++k) fresh &= (w[i][k] & kHi) == ep;
+        if (fresh) break;
+        if (n == kMaxPolls) {
+          lost = true;
+          break;
+        }
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+          for (int k = 0; k < 6; ++k)
+            if ((w[i][k] & kHi) != ep)
+              w[i][k] = __hip_atomic_load(word(i, k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        const int q = sub + i * NSUB;
+        if (q < kpg) {
+          float v[6];
+          if (q == part) {
+            const float* e = own + pair * 6;
+            v[0] = e[2]; v[1] = e[3]; v[2] = e[4]; v[3] = e[5]; v[4] = e[0]; v[5] = e[1];
+          } else {
+#pragma unroll
+            for (int k = 0; k < 6; ++k) v[k] = __builtin_bit_cast(float, (unsigned)w[i][k]);
+          }
+          const float mn = fmaxf(mx, v[4]);
+          const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+          const float wn = v[4] == -INFINITY ? 0.f : fast_exp2(v[4] - mn);
+          lt = lt * wo + v[5] * wn;
+          at = at * wo + f32x4{v[0], v[1], v[2], v[3]} * wn;
+          mx = mn;
+        }
+      }
+    }
+    if constexpr (NSUB > 1) {
+      float* tmp = reinterpret_cast<float*>(lds_dyn + C::L_TMP);
+      if (sub < NSUB) {
+        tmp[(sub * NP + pair) * 6 + 0] = mx;
+        tmp[(sub * NP + pair) * 6 + 1] = lost ? NAN : lt;  // a lost record makes the output NaN
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) tmp[(sub * NP + pair) * 6 + 2 + jj] = at[jj];
+      }
+      wg_barrier();
+      if (sub == 0) {
+#pragma unroll
+        for (int s2 = 1; s2 < NSUB; ++s2) {
+          const float* e = tmp + (s2 * NP + pair) * 6;
+          const float mn = fmaxf(mx, e[0]);
+          const float wo = mx == -INFINITY ? 0.f : fast_exp2(mx - mn);
+          const float wn = e[0] == -INFINITY ? 0.f : fast_exp2(e[0] - mn);
+          lt = lt * wo + e[1] * wn;
+          at = at * wo + f32x4{e[2], e[3], e[4], e[5]} * wn;
+          mx = mn;
+        }
+      }
+    }
+    if (sub == 0 && hs < G) {
+      float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
+      gstore<f32x4>(o + 4 * cq, lost ? f32x4{NAN, NAN, NAN, NAN} : at * (1.f / lt));
+    }
+    if (tt == 0) __hip_atomic_store(gcnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
   {
     // wave wv combines head slots wv + NWV t; lane = (slot t, float4 cq)
     constexpr int SPW = (HSL + NWV - 1) / NWV;  // head slots per wave
@@ -518,6 +658,25 @@ void decode_kernel(const DecodeParams p) {
                                               (int64_t)(head0 + hs) * o_s1);
           gstore<f32x4>(o + 4 * cq, at * (1.f / lt));
         }
+      } else if (merger) {
+        float* e = own + (hs * (D / 4) + cq) * 6;
+        e[0] = mx;
+        e[1] = lt;
+        *reinterpret_cast<f32x2*>(e + 2) = f32x2{at[0], at[1]};
+        *reinterpret_cast<f32x2*>(e + 4) = f32x2{at[2], at[3]};
+      } else if (early) {
+        // 64-bit words (value, epoch): word hs (D + 2) + d for acc, + D for
+        // m, + D + 1 for l. An aligned 64-bit access does not tear, so a
+        // reader that sees this launch's epoch in a word has that word's value.
+        unsigned long long* rw = recw + (int64_t)wg * (C::REC / 2) + hs * (D + 2);
+        auto pk = [&](float v) { return ep | __builtin_bit_cast(unsigned, v); };
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          __hip_atomic_store(rw + 4 * cq + c, pk(at[c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (cq == 0) {
+          __hip_atomic_store(rw + D, pk(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(rw + D + 1, pk(lt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       } else {
         const unsigned r0 = (unsigned)(wg * C::REC * 4);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, at), recr,
@@ -528,8 +687,12 @@ void decode_kernel(const DecodeParams p) {
       }
     }
   }
+  if (kpg == 1 || (early && !merger)) return;
+  if (merger) {
+    merge_early();
+    return;
+  }
   wait_vmem<0>();  // the record stores have completed
-  if (kpg == 1) return;
 
   // Cross-workgroup combine. The group's workgroups form teams of up to TEAM
   // (as many records as one merge round below reads). The last workgroup to
@@ -538,16 +701,13 @@ void decode_kernel(const DecodeParams p) {
   // and the last team to arrive merges the team records and writes O. Each
   // merger re-arms the counter it completed. Counters of group gid:
   // cnt[gid * cst] (teams), cnt[gid * cst + 1 + team].
-  constexpr int NP = HSL * D / 4;             // (head slot, float4) pairs
-  constexpr int NSUB = NWV * kWave / NP;      // record subsets
+  constexpr int NP = C::NP, NSUB = C::NSUB;
   static_assert(NSUB >= 1, "one pair per thread");
   constexpr int RB8 = 8;                      // records per subset requested at once
   constexpr int TEAM = NSUB * RB8;            // records one round reads
   const int n_teams = (kpg + TEAM - 1) / TEAM;
   const int team = part / TEAM, team_first = team * TEAM;
   const int team_n = min(TEAM, kpg - team_first);
-  unsigned* const gcnt = p.cnt + (int64_t)gid * p.cst;
-  unsigned* flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
   // arrive at counter c, expecting n arrivals: true for the last one
   auto arrive = [&](unsigned* c, int n) __attribute__((always_inline)) {
     wg_barrier();
@@ -697,7 +857,7 @@ int decode_group_size(int n_rep) {
 
 size_t decode_record_floats(int head_dim, int group) {
   const int hsl = group > 4 ? 8 : 4;
-  return (size_t)((hsl * (head_dim + 2) + 3) & ~3);
+  return (size_t)(2 * hsl * (head_dim + 2));  // room for the early protocol's 64-bit words
 }
 
 hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,

@@ -62,6 +62,7 @@ struct State {
   // demand, never shrunk.
   char* ws = nullptr;
   size_t ws_bytes = 0;
+  uint32_t epoch = 0;  // stamp of the last decode launch
   int n_cu = 0;  // compute units of the device
 };
 State g;
@@ -114,7 +115,7 @@ int ensure_workspace(size_t rec_bytes) {
   void* p = nullptr;
   int rc = dev_alloc(&p, need, "workspace");
   if (rc) return rc;
-  hipError_t e = hipMemset(p, 0, kCounterBytes);
+  hipError_t e = hipMemset(p, 0, need);  // counters zero, record stamps 0 (no launch's epoch)
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     dev_free(p, need);
@@ -126,6 +127,13 @@ int ensure_workspace(size_t rec_bytes) {
 }
 
 unsigned* ws_counters() { return reinterpret_cast<unsigned*>(g.ws); }
+
+// The stamp of the next decode launch: never 0, the stamp of zeroed records.
+uint32_t next_epoch() {
+  std::lock_guard<std::mutex> lk(g.mu);
+  if (++g.epoch == 0) g.epoch = 1;
+  return g.epoch;
+}
 float* ws_records() { return reinterpret_cast<float*>(g.ws + kCounterBytes); }
 
 int env_int(const char* name, int dflt) {
@@ -350,6 +358,10 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
     p.scale_log2e = items[0].scale * kLog2e;
     p.rec = ws_records();
     p.cnt = ws_counters();
+    // Early merging needs every workgroup of the launch resident at once (one
+    // per CU, the LDS ring fills a CU): a merger waits for its group's others.
+    p.early = plan.n_wg <= g.n_cu && env_int("MI_HIP_DECODE_EARLY", 1) != 0;
+    p.epoch = next_epoch();
     hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     base += cnt;
