@@ -530,8 +530,6 @@ void decode_kernel(const DecodeParams p) {
   }
   wg_barrier();
   const bool merger = early && __builtin_amdgcn_readfirstlane(flag[0]) != 0;
-  unsigned long long* const recw = reinterpret_cast<unsigned long long*>(p.rec);
-  const unsigned long long ep = (unsigned long long)p.epoch << 32;
   float* const own = reinterpret_cast<float*>(lds_dyn + C::L_OWN);
 
   // The early merger: every part's partial in part order (its own from LDS,
@@ -545,7 +543,6 @@ void decode_kernel(const DecodeParams p) {
     constexpr int NP = C::NP, NSUB = C::NSUB;
     constexpr int RB = (kDecodeEarlyMax + NSUB - 1) / NSUB;  // parts per subset
     constexpr int kMaxPolls = 1 << 22;
-    constexpr unsigned long long kHi = 0xffffffff00000000ull;
     wg_barrier();  // the own partial is in LDS
     const int tt = threadIdx.x;
     const int pair = tt % NP, sub = tt / NP;
@@ -554,12 +551,15 @@ void decode_kernel(const DecodeParams p) {
     f32x4 at = {0.f, 0.f, 0.f, 0.f};
     bool lost = false;
     if (sub < NSUB) {
-      const unsigned long long* const g0 = recw + (int64_t)(wg - part) * (C::REC / 2) + hs * (D + 2);
+      // word k of part q's record for this pair: acc values 0-3, then m, l
+      const unsigned long long* const g0 =
+          reinterpret_cast<const unsigned long long*>(p.rec) + (int64_t)(wg - part) * (C::REC / 2) + hs * (D + 2);
       auto word = [&](int i, int k) __attribute__((always_inline)) {
-        return g0 + (int64_t)min(sub + i * NSUB, kpg - 1) * (C::REC / 2) +
-               (k < 4 ? 4 * cq + k : D + (k - 4));
+        return g0 + (int64_t)min(sub + i * NSUB, kpg - 1) * (C::REC / 2) + (k < 4 ? k * (D / 4) + cq : D + (k - 4));
       };
       auto polled = [&](int i) { return sub + i * NSUB < kpg && sub + i * NSUB != part; };
+      const unsigned long long ep = (unsigned long long)p.epoch << 32;
+      constexpr unsigned long long kHi = 0xffffffff00000000ull;
       unsigned long long w[RB][6];
 #pragma unroll
       for (int i = 0; i < RB; ++i)
@@ -665,14 +665,18 @@ void decode_kernel(const DecodeParams p) {
         *reinterpret_cast<f32x2*>(e + 2) = f32x2{at[0], at[1]};
         *reinterpret_cast<f32x2*>(e + 4) = f32x2{at[2], at[3]};
       } else if (early) {
-        // 64-bit words (value, epoch): word hs (D + 2) + d for acc, + D for
-        // m, + D + 1 for l. An aligned 64-bit access does not tear, so a
-        // reader that sees this launch's epoch in a word has that word's value.
-        unsigned long long* rw = recw + (int64_t)wg * (C::REC / 2) + hs * (D + 2);
+        // 64-bit words (value bits, launch epoch), written and read with 64-bit
+        // agent-scope atomics (wider accesses may split): acc value c of pair
+        // (hs, cq) at word hs (D + 2) + c D/4 + cq (consecutive lanes, whole
+        // sectors), m at hs (D + 2) + D, l at + D + 1. A reader that sees this
+        // launch's epoch in a word has that word's value.
+        unsigned long long* const rw = reinterpret_cast<unsigned long long*>(p.rec) +
+                                       (int64_t)wg * (C::REC / 2) + hs * (D + 2);
+        const unsigned long long ep = (unsigned long long)p.epoch << 32;
         auto pk = [&](float v) { return ep | __builtin_bit_cast(unsigned, v); };
 #pragma unroll
         for (int c = 0; c < 4; ++c)
-          __hip_atomic_store(rw + 4 * cq + c, pk(at[c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(rw + c * (D / 4) + cq, pk(at[c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (cq == 0) {
           __hip_atomic_store(rw + D, pk(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(rw + D + 1, pk(lt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -116,8 +116,12 @@ def test_decode_qwen7b_shape_f16_cache(hip, stream, oracle):
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
 
 
-def test_decode_batch_24_layers(hip, stream, oracle):
+@pytest.mark.parametrize("early", ["1", "0"])
+def test_decode_batch_24_layers(hip, stream, oracle, monkeypatch, early):
+    # both cross-workgroup combines at the headline shape (5 workgroups per
+    # group): the first finisher polling stamped records, and the counters
     import torch
+    monkeypatch.setenv("MI_HIP_DECODE_EARLY", early)
     n_layers, n_kv = 24, 4096
     qs, ks, vs, outs, items = [], [], [], [], []
     for layer in range(n_layers):
