@@ -58,6 +58,11 @@ struct RopeAppend {
   int64_t c_s1, c_s2;
   int32_t n_tokens, n_head, n_head_kv, head_dim, n_past, n_dims;
   float freq[kRopeMaxPairs];
+  // Optional table of (cos, sin) pairs, float2 at [pos * n_dims / 2 + p],
+  // covering every position the launch touches: the angles' cosine and sine
+  // as the host's libm returns them (the engine's own values), replacing the
+  // device's correctly rounded ones.
+  const float* cs = nullptr;
 };
 hipError_t launch_rope_node(const RopeNode& p, hipStream_t stream);
 hipError_t launch_rope_append(const RopeAppend& p, bool f16, hipStream_t stream);
@@ -76,6 +81,11 @@ struct Q8MulMat {
   char* dst;      // dst(i, j) at dst_nb0 * i + dst_nb1 * j
   int64_t w_nb1, a_nb1, dst_nb0, dst_nb1;
   int64_t k, n, m;
+  // Optional F32 term added to each product after it is complete (a bias with
+  // add_nb1 = 0, or a residual; it may alias dst): dst(i, j) = dot + add(i, j),
+  // the engine's separate ADD node (src/ops_cpu.cpp:172-175) fused.
+  const char* add = nullptr;
+  int64_t add_nb0 = 0, add_nb1 = 0;
 };
 hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream);
 hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream);
@@ -86,5 +96,29 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream);
 hipError_t launch_kv_append(char* dst, int64_t dst_s1, int64_t dst_s2, bool dst_f16,
                             const char* src, const int64_t src_nb[3], int head_dim,
                             int n_head_kv, int pos0, int n_tokens, hipStream_t stream);
+
+// attn_exact.hip: the attention triple in the reference's operation order
+// (F32 K/V, head_dim a multiple of 4, n_past + n_tokens <= kExactMaxKeys).
+constexpr int kExactMaxKeys = 32768;
+struct ExactAttn {
+  const char* q;  // [head_dim, n_head, n_tokens], byte strides q_s1 (head), q_s2 (token)
+  const char* k;  // cache rows: k_s1 (KV head), k_s2 (position)
+  const char* v;
+  char* out;      // [head_dim, n_head, n_tokens], o_s1, o_s2
+  int64_t q_s1, q_s2, k_s1, k_s2, v_s1, v_s2, o_s1, o_s2;
+  int32_t n_head, n_rep, n_past, n_tokens, head_dim;
+  float scale;
+};
+hipError_t launch_attn_exact(const ExactAttn& p, hipStream_t stream);
+
+// Host helpers of the library's entry points (runtime.hip), for the other
+// host files: the thread's last-error message, the accounted device
+// allocator, selecting the library's device, and its compute-unit count.
+int rt_fail(int code, const char* msg);
+int rt_hip_fail(hipError_t e, const char* what);
+int rt_alloc(void** p, size_t bytes, const char* what);
+void rt_free(void* p, size_t bytes);
+int rt_bind();
+int rt_n_cu();
 
 }  // namespace mi

@@ -101,8 +101,10 @@ __global__ __launch_bounds__(256) void mul_mat_q8_0_kernel(const Q8MulMat p) {
         float s = acc[c] + __shfl_xor(acc[c], 4, 8);
         s = s + __shfl_xor(s, 1, 8);
         s = s + __shfl_xor(s, 2, 8);
-        if (live && l == 0)
+        if (live && l == 0) {
+          if (p.add) s = s + gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1);
           gstore<float>(p.dst + row * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
+        }
       }
     }
   }
@@ -205,6 +207,15 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       t = t + __shfl_xor(t, 2, 8);
       acc[c] = t;
     }
+    // the optional added term: its loads finish (vmcnt 0, which also drains
+    // the other slot's refill) before the stores, so the fixed waits still
+    // count exactly M stores and 8 loads per iteration
+    if (p.add) {
+#pragma unroll
+      for (int c = 0; c < M; ++c)
+        if (row < p.n && l == 0) acc[c] = acc[c] + gload<float>(p.add + row * p.add_nb0 + c * p.add_nb1);
+      wait_vmem<0>();
+    }
     // the slot's reads are done before it is refilled; then M stores (row 0
     // of a group always exists, so every store instruction issues), 8 loads
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -214,6 +225,86 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     refill(s, g + 2 * stride);
   }
   wait_vmem<0>();
+}
+
+// The staged form, for rows longer than the ring's slots (e.g. a 4864-wide
+// FFN down projection) and for more than kQ8Cols columns (a prompt's
+// tokens): one wave per group of 8 rows copies the group's rows (contiguous
+// in memory) into LDS with 16-byte loads, then, per chunk of up to kQ8Cols
+// columns, stages the chunk's activation blocks beside them; lane (row r =
+// lane / 8, accumulator l = lane % 8) walks its row's blocks in order from
+// LDS. Weights are read from HBM once however many columns there are.
+constexpr int kQ8StageLdsMax = 96 * 1024;
+
+__host__ __device__ inline int64_t q8_stage_lds_bytes(int64_t w_nb1, int64_t k) {
+  return ((8 * w_nb1 + 15) & ~int64_t(15)) + kQ8Cols * (k / 32) * 36;
+}
+
+__global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulMat p) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char stage_lds[];
+  const lds_t* const lds = (const lds_t*)stage_lds;
+  const int lane = threadIdx.x;
+  const int64_t g = blockIdx.x;
+  const int nrows = (int)min<int64_t>(8, p.n - g * 8);
+  // the group's bytes end at its last row's last block (rows may be padded)
+  const int64_t wbytes = (nrows - 1) * p.w_nb1 + p.k / 32 * 34;  // a multiple of 2
+  const char* const wsrc = p.w + g * 8 * p.w_nb1;
+  const int64_t w16 = wbytes & ~int64_t(15);
+  // the group's rows: 16-byte pieces, then the 2-byte tail
+#pragma unroll 4
+  for (int64_t o = 16 * lane; o < w16; o += 16 * kWave)
+    lds_store<u32x4>((lds_t*)(stage_lds + o), gload<u32x4>(wsrc + o));
+  for (int64_t o = w16 + 2 * lane; o < wbytes; o += 2 * kWave)
+    lds_store<unsigned short>((lds_t*)(stage_lds + o), gload<unsigned short>(wsrc + o));
+  const int nblk = (int)(p.k / 32);
+  const int abytes = nblk * 36;
+  const int64_t act_off = (8 * p.w_nb1 + 15) & ~int64_t(15);
+  const int l = lane & 7, r = lane >> 3;
+  const int64_t row = g * 8 + r;
+  const bool live = r < nrows;
+  const lds_t* const w = lds + (live ? r : 0) * p.w_nb1;
+  for (int64_t c0 = 0; c0 < p.m; c0 += kQ8Cols) {
+    const int nc = (int)min<int64_t>(kQ8Cols, p.m - c0);
+    __syncthreads();  // the previous chunk's activation reads are done
+    for (int i = lane; i < nc * abytes / 4; i += kWave) {
+      const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
+      lds_store<unsigned>((lds_t*)(stage_lds + act_off + c * abytes + o),
+                          gload<unsigned>(p.a + (c0 + c) * p.a_nb1 + o));
+    }
+    __syncthreads();
+    float acc[kQ8Cols];
+#pragma unroll
+    for (int c = 0; c < kQ8Cols; ++c) acc[c] = 0.0f;
+#pragma unroll 4
+    for (int b = 0; b < nblk; ++b) {
+      const lds_t* wb = w + 34 * b;
+      const float wd = (float)__builtin_bit_cast(_Float16, lds_load<unsigned short>(wb));
+      const int wq = (int)((unsigned)lds_load<unsigned short>(wb + 2 + 4 * l) |
+                           ((unsigned)lds_load<unsigned short>(wb + 4 + 4 * l) << 16));
+#pragma unroll
+      for (int c = 0; c < kQ8Cols; ++c) {
+        if (c < nc) {
+          const lds_t* ab = lds + act_off + c * abytes + 36 * b;
+          const float dxdy = wd * lds_load<float>(ab);
+          const int isum = __builtin_amdgcn_sdot4(wq, lds_load<int>(ab + 4 + 4 * l), 0, false);
+          acc[c] = __builtin_fmaf((float)isum, dxdy, acc[c]);
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kQ8Cols; ++c) {
+      if (c < nc) {
+        float s = acc[c] + __shfl_xor(acc[c], 4, 8);
+        s = s + __shfl_xor(s, 1, 8);
+        s = s + __shfl_xor(s, 2, 8);
+        if (live && l == 0) {
+          if (p.add) s = s + gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1);
+          gstore<float>(p.dst + row * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
+        }
+      }
+    }
+  }
 }
 
 hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream) {
@@ -256,6 +347,14 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) 
       case 7: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<7>, dim3(grid), bs, kQ8RingLds, stream, p); break;
       default: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<8>, dim3(grid), bs, kQ8RingLds, stream, p); break;
     }
+  } else if (q8_stage_lds_bytes(p.w_nb1, p.k) <= kQ8StageLdsMax &&
+             reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && (8 * p.w_nb1) % 16 == 0 &&
+             p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void*)&mul_mat_q8_0_staged_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8StageLdsMax);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(mul_mat_q8_0_staged_kernel, dim3((unsigned)((p.n + 7) / 8)), dim3(kWave),
+                       (unsigned)q8_stage_lds_bytes(p.w_nb1, p.k), stream, p);
   } else {
     hipLaunchKernelGGL(mul_mat_q8_0_kernel, dim3((unsigned)((p.n + 31) / 32)), dim3(256), 0, stream,
                        p);

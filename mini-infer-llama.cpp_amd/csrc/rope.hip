@@ -108,7 +108,13 @@ __global__ void rope_append_kernel(const RopeAppend p) {
     e0 = j;
     e1 = j + half;
     float c, s;
-    rope_angle(pos, p.freq[j], c, s);
+    if (p.cs) {
+      const float2 cs = *reinterpret_cast<const float2*>(p.cs + 2 * ((int64_t)pos * half + j));
+      c = cs.x;
+      s = cs.y;
+    } else {
+      rope_angle(pos, p.freq[j], c, s);
+    }
     rope_rotate(ldf(src, e0 * nb[0]), ldf(src, e1 * nb[0]), c, s, y0, y1);
   } else {
     e0 = p.n_dims + 2 * (j - half);

@@ -557,6 +557,15 @@ int fused_args_from_nodes(mi_tensor* kqv, mi_hip_attn_args* a) {
 
 }  // namespace
 
+namespace mi {
+int rt_fail(int code, const char* msg) { return fail(code, "%s", msg); }
+int rt_hip_fail(hipError_t e, const char* what) { return hip_fail(e, what); }
+int rt_alloc(void** p, size_t bytes, const char* what) { return dev_alloc(p, bytes, what); }
+void rt_free(void* p, size_t bytes) { dev_free(p, bytes); }
+int rt_bind() { return bind_device(); }
+int rt_n_cu() { return g.n_cu; }
+}  // namespace mi
+
 // ===========================================================================
 // C ABI
 // ===========================================================================

@@ -28,6 +28,9 @@ MI_OP_ATTN_KQV = 17
 
 MI_TENSOR_FLAG_KV = 1 << 3
 
+MI_HIP_QWEN2_ATTN_FUSED = 0
+MI_HIP_QWEN2_ATTN_REFERENCE_ORDER = 1
+
 STATUS = {0: "OK", 1: "E_INVALID", 2: "E_NODEVICE", 3: "E_RUNTIME", 4: "E_NOMEM",
           5: "E_UNSUPPORTED", 6: "E_STATE"}
 
@@ -122,12 +125,22 @@ class RopeArgs(ctypes.Structure):
     ]
 
 
+class Qwen2Hparams(ctypes.Structure):
+    """ABI mirror of mi_hip_qwen2_hparams (include/mi_hip_qwen2.h)."""
+    _fields_ = [("n_vocab", ctypes.c_int32), ("n_embd", ctypes.c_int32),
+                ("n_layer", ctypes.c_int32), ("n_head", ctypes.c_int32),
+                ("n_head_kv", ctypes.c_int32), ("n_ff", ctypes.c_int32),
+                ("head_dim", ctypes.c_int32), ("n_ctx_train", ctypes.c_int32),
+                ("rope_freq_base", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
 class AllocStats(ctypes.Structure):
     _fields_ = [("n_malloc", ctypes.c_uint64), ("n_free", ctypes.c_uint64),
                 ("bytes_live", ctypes.c_uint64), ("bytes_peak", ctypes.c_uint64)]
 
 
-# Every symbol include/mi_hip_attn.h declares, with its ctypes signature.
+# Every symbol include/mi_hip_attn.h and include/mi_hip_qwen2.h declare, with
+# its ctypes signature.
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 SIGNATURES = {
@@ -155,6 +168,17 @@ SIGNATURES = {
     "mi_hip_rope_append": ([ctypes.POINTER(RopeArgs)], _I),
     "mi_hip_graph_prepare": ([ctypes.POINTER(MiCgraph)], _I),
     "mi_hip_compute_forward": ([ctypes.POINTER(MiTensor), _I, _I], _I),
+    "mi_hip_qwen2_load": ([ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32,
+                           ctypes.POINTER(ctypes.c_void_p)], _I),
+    "mi_hip_qwen2_free": ([_P], _I),
+    "mi_hip_qwen2_get_hparams": ([_P, ctypes.POINTER(Qwen2Hparams)], _I),
+    "mi_hip_qwen2_forward": ([_P, ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, ctypes.c_int32,
+                              ctypes.c_int32, ctypes.POINTER(ctypes.c_float),
+                              ctypes.POINTER(ctypes.c_int32)], _I),
+    "mi_hip_qwen2_set_attention": ([_P, ctypes.c_int32], _I),
+    "mi_hip_qwen2_set_timing": ([_P, ctypes.c_int32], _I),
+    "mi_hip_qwen2_get_timing": ([_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                 ctypes.POINTER(ctypes.c_int64)], _I),
 }
 
 

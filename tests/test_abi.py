@@ -22,7 +22,7 @@ def lib():
 
 def declared_symbols():
     names = set()
-    for hdr in ("mi_hip_attn.h",):
+    for hdr in ("mi_hip_attn.h", "mi_hip_qwen2.h"):
         text = open(os.path.join(ROOT, "include", hdr)).read()
         names |= set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(mi_hip_\w+)\(", text, re.M))
     return names

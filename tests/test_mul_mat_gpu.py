@@ -88,6 +88,7 @@ def test_q8_0_reproduces_reference_goldens(hip, stream, golden_manifest):
     (4864, 896, 2),     # ffn_down
     (896, 131, 13),     # rows not a multiple of 32, two column chunks
     (3584, 512, 1),     # Qwen2.5-7B hidden size
+    (896, 1152, 128),   # a 128-token prompt through the stacked Q/K/V rows
 ])
 def test_q8_0_model_shapes_equal_oracle(hip, stream, oracle, k, n, m):
     rng = np.random.default_rng(k + n + m)
@@ -101,12 +102,14 @@ def test_q8_0_model_shapes_equal_oracle(hip, stream, oracle, k, n, m):
     assert np.array_equal(bits(got), bits(want))
 
 
-def test_q8_0_strided_operands(hip, stream, oracle):
+@pytest.mark.parametrize("k,n,m", [(896, 100, 3), (4864, 61, 3)])
+def test_q8_0_strided_operands(hip, stream, oracle, k, n, m):
     # padded weight rows, padded activation columns, a destination column
-    # stride wider than n: only the owned bytes are read or written
+    # stride wider than n: only the owned bytes are read or written (the
+    # second shape takes the LDS-staged form, whose last group ends at its
+    # last row's last block, not at the padded stride)
     import torch
     rng = np.random.default_rng(77)
-    k, n, m = 896, 100, 3
     w = q8_weights(rng, n, k, w_nb1=k // 32 * 34 + 6)
     x = rng.standard_normal((m, k)).astype(np.float32)
     act_nb1 = k // 32 * 36 + 8
