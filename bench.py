@@ -8,7 +8,10 @@ Headline (one "step" = one pass of the hot path over one batch):
   not the 256 MB Infinity Cache.
 Also reported (secondary, same run): prefill-1024 and -4096 causal attention
 TFLOP/s (causal FLOPs 4*D*H*n(n+1)/2), the Qwen2.5-7B-shape F16-cache decode
-at n_kv = 8192, and the engine's per-layer call pattern (24 single launches).
+at n_kv = 8192, the engine's per-layer call pattern (24 single launches), the
+Q8_0 output-projection matvec, and end-to-end greedy generation on the device
+engine (tokens/s, attention time per token, ids against the reference engine,
+the reference CPU engine's own --bench on the host cores beside it).
 The CPU baseline times the reference's three-node path (attn_qk -> softmax ->
 attn_kqv with a barrier per node) on the host cores on a bounded sample.
 
@@ -38,8 +41,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,prefill,d7b,perlayer,q8,copy (copy: the counter "
-                         "calibration workload, only when named)")
+                    help="comma list: decode,prefill,d7b,perlayer,q8,e2e,copy (copy: the "
+                         "counter calibration workload, only when named)")
     return ap.parse_args()
 
 
@@ -198,6 +201,77 @@ def bench_copy(torch, steps, warmup, nbytes=256 << 20):
     return dict(bytes=nbytes, kernel_ms=kern_ms, gbps=2 * nbytes / (kern_ms * 1e-3) / 1e9)
 
 
+E2E_SEED = 1234
+
+
+def bench_e2e(mh):
+    """End-to-end greedy generation (the reference CLI's loop, src/main.cpp:474-495)
+    on the random-init Qwen2.5-0.5B-shaped Q8_0 model: 128 seeded prompt ids,
+    one prefill call, 255 decode calls, n_ctx 2048. Fused attention timed plain
+    (tokens/s) and with per-layer attention events (attention time per token);
+    the reference-order mode's ids are checked against the reference engine's."""
+    import tempfile
+    import qwen2_gguf as gg
+    from qwen2 import Qwen2
+    d = tempfile.mkdtemp(prefix="mi_e2e_")
+    path = os.path.join(d, "qwen05_q8_0.gguf")
+    sha = gg.write_qwen2_q8_0(path, E2E_SEED)
+    prompt = gg.prompt_ids(E2E_SEED, 128, gg.QWEN2_05B["n_vocab"])
+    with open(os.path.join(ROOT, "tests", "golden", "e2e_qwen05_q8_0.json")) as f:
+        gold = json.load(f)
+    out = {"workload": "Qwen2.5-0.5B-shaped random-init Q8_0 GGUF (seed 1234), 128-token prompt, "
+                       "256 greedy ids (1 prefill + 255 decode calls), n_ctx 2048",
+           "model_sha256_ok": sha == gold["model_sha256"]}
+    with Qwen2(path, n_ctx=2048, max_tokens=len(prompt)) as m:
+        for mode, key in ((mh.MI_HIP_QWEN2_ATTN_FUSED, "fused"),
+                          (mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER, "reference_order")):
+            m.set_attention(mode)
+            m.generate(prompt[:8], 4)  # warm-up
+            t0 = time.perf_counter()
+            nxt, _ = m.forward(prompt, n_past=0)
+            t1 = time.perf_counter()
+            ids = [nxt]
+            for i in range(255):
+                nxt, _ = m.forward([nxt], n_past=len(prompt) + i)
+                ids.append(nxt)
+            t2 = time.perf_counter()
+            m.set_timing(True)
+            m.forward(prompt, n_past=0)
+            attn_pf, _, _ = m.timing()
+            m.set_timing(True)
+            nxt = ids[0]
+            for i in range(64):
+                nxt, _ = m.forward([nxt], n_past=len(prompt) + i)
+            attn_dec, _, _ = m.timing()
+            m.set_timing(False)
+            out[key] = {"prefill_ms": round((t1 - t0) * 1e3, 3),
+                        "decode_tok_per_s": round(255 / (t2 - t1), 1),
+                        "decode_ms_per_token": round((t2 - t1) * 1e3 / 255, 4),
+                        "attn_us_per_token": round(attn_dec * 1e3 / 64, 2),
+                        "prefill_attn_us": round(attn_pf * 1e3, 1),
+                        "ids_equal_reference": ids == gold["ids"],
+                        "ids_agree_steps": next((i for i, (a, b) in enumerate(zip(ids, gold["ids"]))
+                                                 if a != b), len(ids))}
+    return out, path, d
+
+
+def cpu_reference_engine(path, prompt_path, threads=16):
+    """The reference CLI (oracle/_ref/mini_infer, built from the reference's own
+    sources) with --bench on the host cores: prefill and decode tokens/s."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "mini_infer")
+    if not os.path.exists(exe):
+        return None
+    import subprocess
+    r = subprocess.run([exe, path, "--prompt-ids", prompt_path, "-c", "2048", "-n", "256", "-t",
+                        str(threads), "--bench"], capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return None
+    kv = dict(t.split("=") for t in r.stdout.split())
+    return {"prefill_tok_per_s": float(kv["prefill_tok_per_s"]),
+            "decode_tok_per_s": float(kv["decode_tok_per_s"]), "threads": threads,
+            "kind": "reference"}
+
+
 def cpu_baseline(n_layers_sample=24, n_kv=4096, target_s=12.0):
     """The reference three-node CPU path on the host cores, on a bounded sample
     of the decode workload: 24 layers' decode attention at n_kv = 4096, passes
@@ -290,6 +364,21 @@ def main():
         print(f"# q8_0 matvec 151936x896: {res['q8']['gbps']:.1f} GB/s "
               f"({res['q8']['kernel_ms'] * 1e3:.2f} us)", file=sys.stderr, flush=True)
 
+    if want("e2e"):
+        res["e2e"], e2e_model, e2e_dir = bench_e2e(mh)
+        f = res["e2e"]["fused"]
+        print(f"# e2e 0.5B Q8_0: fused decode {f['decode_tok_per_s']} tok/s, attention "
+              f"{f['attn_us_per_token']} us/token; reference-order ids equal: "
+              f"{res['e2e']['reference_order']['ids_equal_reference']}", file=sys.stderr, flush=True)
+        if not args.no_cpu:
+            import qwen2_gguf as gg
+            ids_path = os.path.join(e2e_dir, "ids.txt")
+            with open(ids_path, "w") as fh:
+                fh.write(" ".join(map(str, gg.prompt_ids(E2E_SEED, 128, gg.QWEN2_05B["n_vocab"]))))
+            res["e2e"]["cpu_reference_engine"] = cpu_reference_engine(e2e_model, ids_path)
+        import shutil
+        shutil.rmtree(e2e_dir, ignore_errors=True)
+
     if "copy" in only:
         res["copy"] = bench_copy(torch, max(5, args.steps // 10), 2)
         print(f"# copy 256 MiB: {res['copy']['gbps']:.1f} GB/s (read + write)", file=sys.stderr,
@@ -362,6 +451,8 @@ def main():
                                 "frac": round(r["kernel_gbps"] / HBM_PEAK_GBPS, 4)}
     if "per_layer" in res:
         out["decode_per_layer_launch"] = {k: round(v, 3) for k, v in res["per_layer"].items()}
+    if "e2e" in res:
+        out["e2e_qwen05_q8_0"] = res["e2e"]
     print(json.dumps(out))
 
 

@@ -218,4 +218,51 @@ __device__ inline float4 load4<_Float16>(const char* p) {
   return make_float4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
 }
 
+// ---------------------------------------------------------------------------
+// Q8_0 activation blocks and the RMS norm scale, shared by the matrix kernels
+// and the engine (the engine's arithmetic: src/quant.cpp:188-210 and
+// src/ops_cpu.cpp:143-165).
+
+// The RMS norm scale from the ordered sum of squares: mean = sum / E,
+// 1 / sqrt(mean + eps), each a correctly rounded float operation (computed in
+// double, whose single rounding to float is the float operation's).
+__device__ inline float rms_scale(float sumsq, int E, float eps) {
+  const float mean = (float)((double)sumsq / (double)E);
+  const float root = (float)__builtin_sqrt((double)(mean + eps));
+  return (float)(1.0 / (double)root);
+}
+
+// The ordered sum of n squares sq[0..n) (n % 4 == 0, 16-byte aligned), by one lane.
+__device__ inline float ordered_sum(const float* sq, int n) {
+#pragma clang fp contract(off)
+  float s = 0.0f;
+  const float4* q4 = reinterpret_cast<const float4*>(sq);
+#pragma unroll 8
+  for (int i = 0; i < n / 4; ++i) {
+    const float4 v = q4[i];
+    s = s + v.x;
+    s = s + v.y;
+    s = s + v.z;
+    s = s + v.w;
+  }
+  return s;
+}
+
+// One Q8_0_ACT block from 32 lanes (an aligned group of 32 lanes, each holding
+// element lane % 32): returns this lane's int8 and, in d, the block scale
+// (amax / 127), as the engine's row quantiser.
+__device__ inline int q8_lane_quant(float y, float& d) {
+#pragma clang fp contract(off)
+  float amax = fabsf(y);
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) {
+    const float o = __shfl_xor(amax, m, 32);
+    amax = o > amax ? o : amax;
+  }
+  d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
+  int q = (int)__builtin_rintf(y * id);
+  return q > 127 ? 127 : (q < -127 ? -127 : q);
+}
+
 }  // namespace mi

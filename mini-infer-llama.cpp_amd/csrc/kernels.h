@@ -86,7 +86,18 @@ struct Q8MulMat {
   // the engine's separate ADD node (src/ops_cpu.cpp:172-175) fused.
   const char* add = nullptr;
   int64_t add_nb0 = 0, add_nb1 = 0;
+  // Optional activation prologue (streaming form only, q8_ring_form): instead
+  // of Q8_0_ACT blocks at `a`, each workgroup quantises the m F32 columns at x
+  // (x_ld floats apart) itself, after RMS_NORM * norm_w when norm_w is set
+  // (src/ops_cpu.cpp:143-170) -- the separate norm / quantize launches fused.
+  const float* x = nullptr;
+  int64_t x_ld = 0;
+  const float* norm_w = nullptr;
+  float eps = 0.0f;
 };
+// Whether launch_mul_mat_q8_0 takes the streaming form for p (the only form
+// with the activation prologue).
+bool q8_ring_form(const Q8MulMat& p);
 hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream);
 hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream);
 

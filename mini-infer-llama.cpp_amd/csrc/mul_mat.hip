@@ -137,9 +137,37 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
   const int nblk = (int)(p.k / 32);
   const int abytes = nblk * 36;
   char* const act_lds = ring_lds + kQ8RingWaves * 2 * kQ8Slot;
-  for (int i = threadIdx.x; i < M * abytes / 4; i += kQ8RingWaves * kWave) {
-    const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
-    *reinterpret_cast<unsigned*>(act_lds + c * abytes + o) = gload<unsigned>(p.a + c * p.a_nb1 + o);
+  if (!p.x) {
+    for (int i = threadIdx.x; i < M * abytes / 4; i += kQ8RingWaves * kWave) {
+      const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
+      *reinterpret_cast<unsigned*>(act_lds + c * abytes + o) = gload<unsigned>(p.a + c * p.a_nb1 + o);
+    }
+  } else {
+    // the prologue: columns into LDS (the ring slots are free until the first
+    // refill), the norm's ordered sums, then one thread per element in groups
+    // of 32 lanes forming each block
+    __shared__ float s_scale[kQ8Cols];
+    float* const xs = reinterpret_cast<float*>(ring_lds);
+    float* const sq = xs + M * p.k;
+    const int k = (int)p.k;
+    for (int i = threadIdx.x; i < M * k; i += kQ8RingWaves * kWave) {
+      const int c = i / k;
+      const float v = gload<float>(p.x + c * p.x_ld + (i - c * k));
+      xs[i] = v;
+      sq[i] = v * v;
+    }
+    __syncthreads();
+    if (p.norm_w && threadIdx.x < M) s_scale[threadIdx.x] = rms_scale(ordered_sum(sq + threadIdx.x * k, k), k, p.eps);
+    __syncthreads();
+    for (int i = threadIdx.x; i < M * k; i += kQ8RingWaves * kWave) {
+      const int c = i / k, e = i - c * k;
+      const float y = p.norm_w ? (xs[i] * s_scale[c]) * gload<float>(p.norm_w + e) : xs[i];
+      float d;
+      const int q = q8_lane_quant(y, d);
+      char* blk = act_lds + c * abytes + 36 * (e / 32);
+      if ((e & 31) == 0) *reinterpret_cast<float*>(blk) = d;
+      blk[4 + (e & 31)] = (char)q;
+    }
   }
   const int64_t n_groups = (p.n + 7) / 8;
   const int64_t stride = (int64_t)gridDim.x * kQ8RingWaves;
@@ -236,10 +264,16 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
 // LDS. Weights are read from HBM once however many columns there are.
 constexpr int kQ8StageLdsMax = 96 * 1024;
 
+__host__ __device__ inline int64_t round1k(int64_t n) { return (n + 1023) & ~int64_t(1023); }
+// LDS of the staged form: the 8-row group and one chunk of activation columns,
+// each rounded up to whole 1 KB LDS-direct transfers.
 __host__ __device__ inline int64_t q8_stage_lds_bytes(int64_t w_nb1, int64_t k) {
-  return ((8 * w_nb1 + 15) & ~int64_t(15)) + kQ8Cols * (k / 32) * 36;
+  return round1k(8 * w_nb1) + round1k(kQ8Cols * (k / 32) * 36);
 }
 
+// MC: columns per chunk (the host picks min(m, kQ8Cols)); only the last chunk
+// may be partial.
+template <int MC>
 __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulMat p) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) char stage_lds[];
@@ -250,51 +284,85 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
   // the group's bytes end at its last row's last block (rows may be padded)
   const int64_t wbytes = (nrows - 1) * p.w_nb1 + p.k / 32 * 34;  // a multiple of 2
   const char* const wsrc = p.w + g * 8 * p.w_nb1;
-  const int64_t w16 = wbytes & ~int64_t(15);
-  // the group's rows: 16-byte pieces, then the 2-byte tail
-#pragma unroll 4
-  for (int64_t o = 16 * lane; o < w16; o += 16 * kWave)
-    lds_store<u32x4>((lds_t*)(stage_lds + o), gload<u32x4>(wsrc + o));
-  for (int64_t o = w16 + 2 * lane; o < wbytes; o += 2 * kWave)
-    lds_store<unsigned short>((lds_t*)(stage_lds + o), gload<unsigned short>(wsrc + o));
+  // the group's rows straight into LDS, every 1 KB transfer in flight at once
+  // (bytes past the group arrive as zeros from the bounded resource). The
+  // resource's range check is per dword, so it ends at the last whole dword;
+  // a 2-byte tail is copied separately once the transfers have landed.
+  const int64_t wb4 = wbytes & ~int64_t(3);
+  {
+    const rsrc_t r = make_rsrc(wsrc, (unsigned)wb4);
+    const int n1k = (int)((wbytes + 1023) / 1024);
+    for (int i = 0; i < n1k; ++i) dma16(r, (lds_t*)stage_lds + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+  }
   const int nblk = (int)(p.k / 32);
   const int abytes = nblk * 36;
-  const int64_t act_off = (8 * p.w_nb1 + 15) & ~int64_t(15);
+  const int64_t act_off = round1k(8 * p.w_nb1);
+  // contiguous 16-byte aligned columns: a chunk is one range, loaded the same way
+  const bool act_dma = p.a_nb1 == abytes && abytes % 16 == 0 && reinterpret_cast<uintptr_t>(p.a) % 16 == 0;
   const int l = lane & 7, r = lane >> 3;
   const int64_t row = g * 8 + r;
   const bool live = r < nrows;
   const lds_t* const w = lds + (live ? r : 0) * p.w_nb1;
-  for (int64_t c0 = 0; c0 < p.m; c0 += kQ8Cols) {
-    const int nc = (int)min<int64_t>(kQ8Cols, p.m - c0);
+  for (int64_t c0 = 0; c0 < p.m; c0 += MC) {
+    const int nc = (int)min<int64_t>(MC, p.m - c0);
     __syncthreads();  // the previous chunk's activation reads are done
-    for (int i = lane; i < nc * abytes / 4; i += kWave) {
-      const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
-      lds_store<unsigned>((lds_t*)(stage_lds + act_off + c * abytes + o),
-                          gload<unsigned>(p.a + (c0 + c) * p.a_nb1 + o));
+    if (act_dma) {
+      const int64_t bytes = (int64_t)nc * abytes;
+      const rsrc_t r = make_rsrc(p.a + c0 * p.a_nb1, (unsigned)bytes);
+      const int n1k = (int)((bytes + 1023) / 1024);
+      for (int i = 0; i < n1k; ++i)
+        dma16(r, (lds_t*)stage_lds + act_off + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+    } else {
+      for (int i = lane; i < nc * abytes / 4; i += kWave) {
+        const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
+        lds_store<unsigned>((lds_t*)(stage_lds + act_off + c * abytes + o),
+                            gload<unsigned>(p.a + (c0 + c) * p.a_nb1 + o));
+      }
     }
+    wait_vmem<0>();  // the LDS-direct transfers have landed
+    if (c0 == 0 && wb4 != wbytes && lane == 0)
+      lds_store<unsigned short>((lds_t*)(stage_lds + wb4), gload<unsigned short>(wsrc + wb4));
     __syncthreads();
-    float acc[kQ8Cols];
+    float acc[MC];
 #pragma unroll
-    for (int c = 0; c < kQ8Cols; ++c) acc[c] = 0.0f;
-#pragma unroll 4
-    for (int b = 0; b < nblk; ++b) {
-      const lds_t* wb = w + 34 * b;
-      const float wd = (float)__builtin_bit_cast(_Float16, lds_load<unsigned short>(wb));
-      const int wq = (int)((unsigned)lds_load<unsigned short>(wb + 2 + 4 * l) |
-                           ((unsigned)lds_load<unsigned short>(wb + 4 + 4 * l) << 16));
+    for (int c = 0; c < MC; ++c) acc[c] = 0.0f;
+    const lds_t* const act = lds + act_off + 4 + 4 * l;
+    // blocks in order; 8 at a time with all their LDS reads issued first, so
+    // their latency overlaps the chain of multiply-adds (a tail of fewer than
+    // 8 re-reads the last block and does not add it)
+    for (int b0 = 0; b0 < nblk; b0 += 8) {
+      float wd[8];
+      int wq[8];
 #pragma unroll
-      for (int c = 0; c < kQ8Cols; ++c) {
-        if (c < nc) {
-          const lds_t* ab = lds + act_off + c * abytes + 36 * b;
-          const float dxdy = wd * lds_load<float>(ab);
-          const int isum = __builtin_amdgcn_sdot4(wq, lds_load<int>(ab + 4 + 4 * l), 0, false);
-          acc[c] = __builtin_fmaf((float)isum, dxdy, acc[c]);
+      for (int u = 0; u < 8; ++u) {
+        const lds_t* wb = w + 34 * min(b0 + u, nblk - 1);
+        wd[u] = (float)__builtin_bit_cast(_Float16, lds_load<unsigned short>(wb));
+        wq[u] = (int)((unsigned)lds_load<unsigned short>(wb + 2 + 4 * l) |
+                      ((unsigned)lds_load<unsigned short>(wb + 4 + 4 * l) << 16));
+      }
+#pragma unroll
+      for (int c = 0; c < MC; ++c) {
+        if (MC == 1 || c < nc) {
+          float ad[8];
+          int aq[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int bb = min(b0 + u, nblk - 1);
+            ad[u] = lds_load<float>(act - 4 - 4 * l + c * abytes + 36 * bb);
+            aq[u] = lds_load<int>(act + c * abytes + 36 * bb);
+          }
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const float r = __builtin_fmaf((float)__builtin_amdgcn_sdot4(wq[u], aq[u], 0, false),
+                                           wd[u] * ad[u], acc[c]);
+            acc[c] = b0 + u < nblk ? r : acc[c];
+          }
         }
       }
     }
 #pragma unroll
-    for (int c = 0; c < kQ8Cols; ++c) {
-      if (c < nc) {
+    for (int c = 0; c < MC; ++c) {
+      if (MC == 1 || c < nc) {
         float s = acc[c] + __shfl_xor(acc[c], 4, 8);
         s = s + __shfl_xor(s, 1, 8);
         s = s + __shfl_xor(s, 2, 8);
@@ -315,12 +383,20 @@ hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+bool q8_ring_form(const Q8MulMat& p) {
+  const bool act_ok = p.x ? (p.x_ld >= p.k && reinterpret_cast<uintptr_t>(p.x) % 4 == 0)
+                          : (p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0);
+  // rows 4-byte aligned: every group's byte range ends on a whole dword (the
+  // resource's range check is per dword)
+  return p.w_nb1 <= kQ8RowBytesMax && p.k <= 960 && p.m <= kQ8Cols && (8 * p.w_nb1) % 16 == 0 &&
+         p.w_nb1 % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && act_ok && p.n * p.w_nb1 < (int64_t)1 << 40;
+}
+
 hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) {
   if (p.n == 0 || p.m == 0) return hipSuccess;
-  const bool rows_form = p.w_nb1 <= kQ8RowBytesMax && p.k <= 960 && p.m <= kQ8Cols &&
-                         (8 * p.w_nb1) % 16 == 0 && reinterpret_cast<uintptr_t>(p.w) % 16 == 0 &&
-                         p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0 &&
-                         p.n * p.w_nb1 < (int64_t)1 << 40;
+  const bool rows_form = q8_ring_form(p);
+  if (p.x && !rows_form) return hipErrorInvalidValue;  // the prologue exists in the streaming form only
   if (rows_form) {
     static const hipError_t attr = [] {
       hipError_t e = hipSuccess;
@@ -350,11 +426,21 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) 
   } else if (q8_stage_lds_bytes(p.w_nb1, p.k) <= kQ8StageLdsMax &&
              reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && (8 * p.w_nb1) % 16 == 0 &&
              p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0) {
-    static const hipError_t attr = hipFuncSetAttribute(
-        (const void*)&mul_mat_q8_0_staged_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8StageLdsMax);
+    static const hipError_t attr = [] {
+      hipError_t e = hipSuccess;
+      const void* fns[2] = {(const void*)&mul_mat_q8_0_staged_kernel<1>,
+                            (const void*)&mul_mat_q8_0_staged_kernel<kQ8Cols>};
+      for (const void* f : fns)
+        if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8StageLdsMax);
+      return e;
+    }();
     if (attr != hipSuccess) return attr;
-    hipLaunchKernelGGL(mul_mat_q8_0_staged_kernel, dim3((unsigned)((p.n + 7) / 8)), dim3(kWave),
-                       (unsigned)q8_stage_lds_bytes(p.w_nb1, p.k), stream, p);
+    const dim3 grid((unsigned)((p.n + 7) / 8));
+    const unsigned lds = (unsigned)q8_stage_lds_bytes(p.w_nb1, p.k);
+    if (p.m == 1)
+      hipLaunchKernelGGL(mul_mat_q8_0_staged_kernel<1>, grid, dim3(kWave), lds, stream, p);
+    else
+      hipLaunchKernelGGL(mul_mat_q8_0_staged_kernel<kQ8Cols>, grid, dim3(kWave), lds, stream, p);
   } else {
     hipLaunchKernelGGL(mul_mat_q8_0_kernel, dim3((unsigned)((p.n + 31) / 32)), dim3(256), 0, stream,
                        p);

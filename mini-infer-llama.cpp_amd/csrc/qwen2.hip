@@ -45,32 +45,6 @@ __constant__ uint64_t kExpfTab[32] = MI_EXPF_TABLE;
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxE = 8192;  // widest normalised row (LDS copy of one column)
 
-// 32 values -> one Q8_0_ACT block (float scale, 32 int8), the activation
-// quantiser of src/quant.cpp:188-210 (same arithmetic as mul_mat.hip's).
-__device__ inline void q8_store_block(const float (&y)[32], char* dst) {
-#pragma clang fp contract(off)
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const float av = fabsf(y[j]);
-    if (av > amax) amax = av;
-  }
-  const float d = amax / 127.0f;
-  const float id = d != 0.0f ? 1.0f / d : 0.0f;
-  gstore<float>(dst, d);
-#pragma unroll
-  for (int j = 0; j < 32; j += 4) {
-    unsigned word = 0;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      int q = (int)__builtin_rintf(y[j + t] * id);
-      q = q > 127 ? 127 : (q < -127 ? -127 : q);
-      word |= (unsigned)(q & 0xff) << (8 * t);
-    }
-    gstore<unsigned>(dst + 4 + j, word);
-  }
-}
-
 // GET_ROWS of token_embd (src/ops_cpu.cpp:102-132): x[:, j] = row ids[j],
 // dequantised as (float)q * fp16 scale for Q8_0.
 __global__ void embed_kernel(const char* w, int64_t row_bytes, int type, const int32_t* ids,
@@ -93,67 +67,51 @@ __global__ void embed_kernel(const char* w, int64_t row_bytes, int type, const i
 }
 
 // RMS_NORM then MUL by the weight (src/ops_cpu.cpp:143-170), quantised to
-// Q8_0_ACT blocks. One workgroup per column. The sum of squares runs in the
-// reference's order (one lane, element by element, each square rounded), so
-// the scale is the reference's to the bit: mean = sum / E, s = sqrt(mean +
-// eps), scale = 1 / s, each a correctly rounded float operation (computed in
-// double, whose one rounding to float is then the float operation's).
+// Q8_0_ACT blocks. One workgroup per column: squares in parallel, their sum in
+// the reference's order by one lane (so the scale is the reference's to the
+// bit), then one thread per element, 32 lanes to a block.
 __global__ __launch_bounds__(kNormThreads) void norm_q8_kernel(const float* x, int64_t x_ld,
                                                                const float* w, float eps, char* aq,
                                                                int64_t aq_ld, int E) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) float row[kNormMaxE];
+  __shared__ __attribute__((aligned(16))) float sq[kNormMaxE];
   __shared__ float s_scale;
   const float* xr = x + (int64_t)blockIdx.x * x_ld;
-  for (int i = threadIdx.x; i < E; i += kNormThreads) row[i] = gload<float>(xr + i);
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.0f;
-    const float4* r4 = reinterpret_cast<const float4*>(row);
-#pragma unroll 4
-    for (int i = 0; i < E / 4; ++i) {
-      const float4 v = r4[i];
-      s = s + v.x * v.x;
-      s = s + v.y * v.y;
-      s = s + v.z * v.z;
-      s = s + v.w * v.w;
-    }
-    const float mean = (float)((double)s / (double)E);
-    const float root = (float)sqrt((double)(mean + eps));
-    s_scale = (float)(1.0 / (double)root);
+  for (int i = threadIdx.x; i < E; i += kNormThreads) {
+    const float v = gload<float>(xr + i);
+    sq[i] = v * v;
   }
+  __syncthreads();
+  if (threadIdx.x == 0) s_scale = rms_scale(ordered_sum(sq, E), E, eps);
   __syncthreads();
   const float scale = s_scale;
   char* dst = aq + (int64_t)blockIdx.x * aq_ld;
-  for (int b = threadIdx.x; b < E / 32; b += kNormThreads) {
-    float y[32];
-#pragma unroll
-    for (int j = 0; j < 32; ++j) y[j] = (row[32 * b + j] * scale) * gload<float>(w + 32 * b + j);
-    q8_store_block(y, dst + 36 * b);
+  for (int i = threadIdx.x; i < E; i += kNormThreads) {  // E % 32 == 0: whole 32-lane groups
+    float d;
+    const int q = q8_lane_quant((gload<float>(xr + i) * scale) * gload<float>(w + i), d);
+    if ((i & 31) == 0) gstore<float>(dst + 36 * (i / 32), d);
+    gstore<signed char>(dst + 36 * (i / 32) + 4 + (i & 31), (signed char)q);
   }
 }
 
 // SILU(gate) * up (src/ops_cpu.cpp:134-141, 167-170), quantised to Q8_0_ACT
-// blocks; one thread per block of 32. silu(x) = x / (1 + expf(-x)) with the
-// host C library's expf (libm_ref.h), so every value is the engine's.
+// blocks; one thread per element, 32 lanes to a block. silu(x) = x / (1 +
+// expf(-x)) with the host C library's expf (libm_ref.h), so every value is the
+// engine's.
 __global__ void silu_mul_q8_kernel(const float* gu, int64_t gu_ld, int F, char* aq, int64_t aq_ld,
                                    int T) {
 #pragma clang fp contract(off)
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int nb = F / 32;
-  if (idx >= (int64_t)T * nb) return;
-  const int64_t col = idx / nb;
-  const int b = (int)(idx - col * nb);
-  const float* g = gu + col * gu_ld + 32 * b;
-  const float* u = g + F;
-  float y[32];
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const float xv = gload<float>(g + j);
-    const float e = expf_ref(-xv, kExpfTab);
-    y[j] = (xv / (1.0f + e)) * gload<float>(u + j);
-  }
-  q8_store_block(y, aq + col * aq_ld + 36 * b);
+  if (idx >= (int64_t)T * F) return;  // T * F % 32 == 0: whole 32-lane groups leave together
+  const int64_t col = idx / F;
+  const int e = (int)(idx - col * F);
+  const float g = gload<float>(gu + col * gu_ld + e);
+  const float y = (g / (1.0f + expf_ref(-g, kExpfTab))) * gload<float>(gu + col * gu_ld + F + e);
+  float d;
+  const int q = q8_lane_quant(y, d);
+  char* blk = aq + col * aq_ld + 36 * (e / 32);
+  if ((e & 31) == 0) gstore<float>(blk, d);
+  gstore<signed char>(blk + 4 + (e & 31), (signed char)q);
 }
 
 // mi_qwen2_sample_greedy (src/model_qwen2.cpp:690-700): the first index of
@@ -442,12 +400,23 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   return MI_HIP_OK;
 }
 
-int matmul(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, int64_t k,
-           const char* act, int64_t m_cols, float* dst, int64_t dst_ld, const float* add,
-           int64_t add_ld) {
+// The activation of a projection: Q8_0_ACT blocks already in m->aq, or F32
+// columns x (x_ld floats apart) to quantise, after RMS_NORM * norm_w if set.
+struct Act {
+  const float* x;
+  const float* norm_w;
+};
+
+int quantize_cols(const mi_hip_qwen2* m, const float* src, int64_t ne0, int64_t cols, char* dst);
+
+// dst[:, j] (+)= W . act[:, j] for j < m_cols. Decode-sized calls take the
+// streaming matrix kernel with the norm / quantisation as its prologue (one
+// launch); the others run the norm or quantize kernel into m->aq first.
+int proj(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, int64_t k, Act act,
+         int64_t m_cols, float* dst, int64_t dst_ld, const float* add, int64_t add_ld) {
   mi::Q8MulMat p{};
   p.w = w;
-  p.a = act;
+  p.a = m->aq;
   p.dst = reinterpret_cast<char*>(dst);
   p.w_nb1 = row_bytes;
   p.a_nb1 = k / 32 * 36;
@@ -459,6 +428,24 @@ int matmul(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, i
   p.add = reinterpret_cast<const char*>(add);
   p.add_nb0 = add ? 4 : 0;
   p.add_nb1 = 4 * add_ld;
+  if (act.x) {
+    p.x = act.x;
+    p.x_ld = k;
+    p.norm_w = act.norm_w;
+    p.eps = m->hp.rms_eps;
+    if (!mi::q8_ring_form(p)) {
+      p.x = nullptr;
+      p.norm_w = nullptr;
+      if (act.norm_w) {
+        hipLaunchKernelGGL(mi::norm_q8_kernel, dim3((unsigned)m_cols), dim3(mi::kNormThreads), 0, m->stream,
+                           act.x, k, act.norm_w, m->hp.rms_eps, m->aq, p.a_nb1, (int)k);
+        Q2_TRY(hipGetLastError(), "norm launch");
+      } else {
+        int rc = quantize_cols(m, act.x, k, m_cols, m->aq);
+        if (rc) return rc;
+      }
+    }
+  }
   hipError_t e = mi::launch_mul_mat_q8_0(p, mi::rt_n_cu(), m->stream);
   return e == hipSuccess ? MI_HIP_OK : mi::rt_hip_fail(e, "qwen2 mul_mat launch");
 }
@@ -486,7 +473,7 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
   const mi_hip_qwen2_hparams& hp = m->hp;
   const int E = hp.n_embd, F = hp.n_ff, hd = hp.head_dim, H = hp.n_head;
   const int64_t qkv_rows = E + 2 * m->kvd;
-  const int64_t ab_e = E / 32 * 36, ab_f = F / 32 * 36;
+  const int64_t ab_f = F / 32 * 36;
   hipStream_t st = m->stream;
   int rc;
   std::memcpy(m->h_ids, tokens, 4 * (size_t)T);
@@ -497,10 +484,8 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
   const float scale = 1.0f / std::sqrt((float)hd);
   for (int l = 0; l < hp.n_layer; ++l) {
     const mi_hip_qwen2::Layer& w = m->layers[l];
-    hipLaunchKernelGGL(mi::norm_q8_kernel, dim3(T), dim3(mi::kNormThreads), 0, st, m->x, (int64_t)E,
-                       w.attn_norm, hp.rms_eps, m->aq, ab_e, E);
-    Q2_TRY(hipGetLastError(), "norm launch");
-    if ((rc = matmul(m, w.wqkv, m->row_e, qkv_rows, E, m->aq, T, m->qkv, qkv_rows, w.bqkv, 0))) return rc;
+    if ((rc = proj(m, w.wqkv, m->row_e, qkv_rows, E, {m->x, w.attn_norm}, T, m->qkv, qkv_rows, w.bqkv, 0)))
+      return rc;
     const size_t nb[3] = {4, 4 * (size_t)hd, 4 * (size_t)qkv_rows};
     {
       // RoPE on Q and K in place, K and V appended at positions n_past.. (one launch)
@@ -575,26 +560,20 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
       return rc;
     }
     if (m->timing) Q2_TRY(hipEventRecord(m->ev[2 * l + 1], st), "hipEventRecord");
-    if ((rc = quantize_cols(m, m->ao, E, T, m->aq))) return rc;
-    if ((rc = matmul(m, w.wo, m->row_e, E, E, m->aq, T, m->x, E, m->x, E))) return rc;
-    hipLaunchKernelGGL(mi::norm_q8_kernel, dim3(T), dim3(mi::kNormThreads), 0, st, m->x, (int64_t)E,
-                       w.ffn_norm, hp.rms_eps, m->aq, ab_e, E);
-    Q2_TRY(hipGetLastError(), "norm launch");
-    if ((rc = matmul(m, w.wgu, m->row_e, 2 * (int64_t)F, E, m->aq, T, m->gu, 2 * (int64_t)F, nullptr, 0)))
+    if ((rc = proj(m, w.wo, m->row_e, E, E, {m->ao, nullptr}, T, m->x, E, m->x, E))) return rc;
+    if ((rc = proj(m, w.wgu, m->row_e, 2 * (int64_t)F, E, {m->x, w.ffn_norm}, T, m->gu, 2 * (int64_t)F,
+                   nullptr, 0)))
       return rc;
-    const int64_t nblk = (int64_t)T * (F / 32);
-    hipLaunchKernelGGL(mi::silu_mul_q8_kernel, dim3((unsigned)((nblk + 255) / 256)), dim3(256), 0, st,
+    const int64_t nel = (int64_t)T * F;
+    hipLaunchKernelGGL(mi::silu_mul_q8_kernel, dim3((unsigned)((nel + 255) / 256)), dim3(256), 0, st,
                        m->gu, 2 * (int64_t)F, F, m->aq, ab_f, T);
     Q2_TRY(hipGetLastError(), "silu launch");
-    if ((rc = matmul(m, w.wdown, m->row_f, E, F, m->aq, T, m->x, E, m->x, E))) return rc;
+    if ((rc = proj(m, w.wdown, m->row_f, E, F, {nullptr, nullptr}, T, m->x, E, m->x, E))) return rc;
   }
   const int first = last_only ? T - 1 : 0;
   const int n_out = T - first;
-  hipLaunchKernelGGL(mi::norm_q8_kernel, dim3(n_out), dim3(mi::kNormThreads), 0, st,
-                     m->x + (int64_t)first * E, (int64_t)E, m->out_norm, hp.rms_eps, m->aq, ab_e, E);
-  Q2_TRY(hipGetLastError(), "norm launch");
-  if ((rc = matmul(m, m->lm_head, m->row_e, hp.n_vocab, E, m->aq, n_out, m->logits, hp.n_vocab,
-                   nullptr, 0)))
+  if ((rc = proj(m, m->lm_head, m->row_e, hp.n_vocab, E, {m->x + (int64_t)first * E, m->out_norm}, n_out,
+                 m->logits, hp.n_vocab, nullptr, 0)))
     return rc;
   hipLaunchKernelGGL(mi::argmax_kernel, dim3(1), dim3(mi::kArgmaxThreads), 0, st,
                      m->logits + (int64_t)(n_out - 1) * hp.n_vocab, hp.n_vocab, m->next);

@@ -89,6 +89,8 @@ def test_q8_0_reproduces_reference_goldens(hip, stream, golden_manifest):
     (896, 131, 13),     # rows not a multiple of 32, two column chunks
     (3584, 512, 1),     # Qwen2.5-7B hidden size
     (896, 1152, 128),   # a 128-token prompt through the stacked Q/K/V rows
+    (96, 9, 2),         # odd block count: 102-byte rows end mid-dword (staged form)
+    (4832, 75, 1),      # 151 blocks per row, a 3-row last group
 ])
 def test_q8_0_model_shapes_equal_oracle(hip, stream, oracle, k, n, m):
     rng = np.random.default_rng(k + n + m)
