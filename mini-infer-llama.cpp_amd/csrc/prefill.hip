@@ -372,6 +372,8 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       if (Xn != Xu) load_q(Xn);  // the running state still belongs to Xu
       wait_vmem<C::WAIT_K>();
       read_k(kk);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the whole A operand at once
+      __builtin_amdgcn_sched_barrier(0);
       const floatx16 sn = qk(kk);
       softmax(sc, Xu, unit_tile(u));
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
