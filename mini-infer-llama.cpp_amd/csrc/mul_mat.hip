@@ -17,6 +17,7 @@
 //    xor exchanges (float addition is commutative, so each partial is the
 //    same value on both lanes that form it).
 #include <algorithm>
+#include <type_traits>
 
 #include "attn_common.h"
 #include "kernels.h"
@@ -125,7 +126,17 @@ constexpr int kQ8RingWaves = 8;
 constexpr int kQ8Slot = 8 * kQ8RowBytesMax;
 constexpr int kQ8MaxBlocks = 30;                   // k <= 960
 constexpr int kQ8ActBytesMax = kQ8Cols * kQ8MaxBlocks * 36;
-constexpr int kQ8RingLds = kQ8RingWaves * 2 * kQ8Slot + kQ8ActBytesMax;
+constexpr int kQ8RingTake = kQ8RingWaves * 2 * kQ8Slot + kQ8ActBytesMax;  // the group counter
+constexpr int kQ8RingLds = kQ8RingTake + 16;
+
+// Returns *c and adds 1 (an LDS atomic). As asm: the compiler's wait insertion
+// would otherwise wait for every LDS-direct load in flight (vmcnt(0)) before
+// an LDS atomic. The counter is never a load target.
+__device__ inline unsigned lds_take(__attribute__((address_space(3))) unsigned* c) {
+  unsigned t;
+  asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(t) : "v"(c), "v"(1u) : "memory");
+  return t;
+}
 
 template <int M>
 __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel(const Q8MulMat p) {
@@ -169,24 +180,36 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       blk[4 + (e & 31)] = (char)q;
     }
   }
+  // This workgroup's contiguous range of 8-row groups; its waves take groups
+  // from an LDS counter as they refill, so a wave served faster takes more
+  // and the waves finish together.
   const int64_t n_groups = (p.n + 7) / 8;
-  const int64_t stride = (int64_t)gridDim.x * kQ8RingWaves;
-  const int64_t g0 = (int64_t)blockIdx.x * kQ8RingWaves + wv;
+  const int64_t glo = n_groups * blockIdx.x / gridDim.x;
+  const int64_t ngw = n_groups * (blockIdx.x + 1) / gridDim.x - glo;
+  __attribute__((address_space(3))) unsigned* const take =
+      reinterpret_cast<__attribute__((address_space(3))) unsigned*>(lds + kQ8RingTake);
   const int64_t total = p.n * p.w_nb1;
   const rsrc_t none = make_rsrc(p.w, 0u);
   lds_t* const slots = lds + wv * 2 * kQ8Slot;
-  auto refill = [&](int s, int64_t g) __attribute__((always_inline)) {
+  // refills slot s with the next group taken; returns it, or -1 past the range
+  auto refill = [&](int s) __attribute__((always_inline)) -> int64_t {
+    unsigned t = 0;
+    if (lane == 0) t = lds_take(take);
+    t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
+    const int64_t g = glo + (int64_t)t;
+    const bool live = t < (unsigned)ngw;
     rsrc_t r = none;
-    if (g < n_groups) {
+    if (live) {
       const int64_t start = g * 8 * p.w_nb1;
       r = make_rsrc(p.w + start, (unsigned)min<int64_t>(8 * p.w_nb1, total - start));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) dma16(r, slots + s * kQ8Slot + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+    return live ? g : -1;
   };
+  if (threadIdx.x == 0) *reinterpret_cast<__attribute__((address_space(3))) unsigned*>(take) = 0u;
   __syncthreads();  // the activation is staged (before the ring requests: the barrier waits for all loads)
-  refill(0, g0);
-  refill(1, g0 + stride);
+  int64_t g_0 = refill(0), g_1 = refill(1);  // the group in each slot, or -1
   const int l = lane & 7, rs = lane >> 3;
   const lds_t* const act = lds + kQ8RingWaves * 2 * kQ8Slot;
   // one column: this lane's activation byte groups and the block scales, in registers
@@ -199,9 +222,12 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       a_q[b] = b < nblk ? lds_load<int>(act + 36 * b + 4 + 4 * l) : 0;
     }
   }
-  int s = 0;
-  for (int64_t g = g0; g < n_groups; g += stride, s ^= 1) {
-    if (g == g0)
+  // slots in turn until the first empty one (a wave's takes increase, so
+  // every later slot is empty too)
+  for (int s = 0, it = 0;; s ^= 1, ++it) {
+    const int64_t g = s ? g_1 : g_0;
+    if (g < 0) break;
+    if (it == 0)
       wait_vmem<8>();
     else
       wait_vmem<M + 8>();
@@ -250,7 +276,11 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
 #pragma unroll
     for (int c = 0; c < M; ++c)
       if (row < p.n && l == 0) gstore<float>(p.dst + row * p.dst_nb0 + c * p.dst_nb1, acc[c]);
-    refill(s, g + 2 * stride);
+    const int64_t gn = refill(s);
+    if (s)
+      g_1 = gn;
+    else
+      g_0 = gn;
   }
   wait_vmem<0>();
 }
