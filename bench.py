@@ -314,9 +314,9 @@ def _cpu_model():
     return "unknown"
 
 
-def measured_traffic():
-    """HBM bytes per decode launch from the committed rocprofv3 PMC summary."""
-    p = os.path.join(ROOT, "profiles", "decode_traffic.json")
+def measured_traffic(name="decode_traffic.json"):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary."""
+    p = os.path.join(ROOT, "profiles", name)
     if os.path.exists(p):
         with open(p) as f:
             return json.load(f).get("bytes_per_launch")
@@ -431,6 +431,7 @@ def main():
             "gbps": round(q8["gbps"], 2), "us": round(q8["kernel_ms"] * 1e3, 2),
             "roofline": {"bound": "hbm", "achieved": round(q8["gbps"], 2), "peak": HBM_PEAK_GBPS,
                          "unit": "GB/s", "frac": round(q8["gbps"] / HBM_PEAK_GBPS, 4),
+                         "traffic": measured_traffic("q8_0_matvec_traffic.json"),
                          "bytes_per_launch": q8["bytes"]},
         }
     if "prefill1024" in res:
