@@ -10,8 +10,9 @@ vocabulary src/gguf.cpp:725-757):
   * keys: general.architecture, general.alignment (32), the qwen2.* hparams,
     tokenizer.ggml.tokens (one placeholder string per id);
   * tensors: token_embd.weight, output_norm.weight and per layer blk.N.*
-    (no output.weight: the lm_head is tied to token_embd, :497-505), each
-    tensor's data at a 32-byte aligned offset of the data section.
+    (by default no output.weight: the lm_head is tied to token_embd,
+    :497-505), each tensor's data at a 32-byte aligned offset of the data
+    section.
 
 Values. Weight matrices and biases are N(0, 0.02), RMSNorm weights are 1.0.
 The normal draws use no libm: element e of tensor t takes
@@ -20,7 +21,8 @@ four 16-bit fields (Irwin-Hall, n = 4) and standardises the sum, so the file
 is a pure function of the seed, identical on every machine. Matrices are then
 quantised to Q8_0 (34-byte blocks: fp16 scale d = amax/127, 32 int8
 round-half-to-even(x/d), src/quant.cpp:129-153, fp16 by round to nearest
-even); 1-D tensors stay F32.
+even); 1-D tensors stay F32; token_embd may instead be F16 or F32 (then with
+a separate Q8_0 output.weight).
 """
 import hashlib
 import os
@@ -29,7 +31,7 @@ import struct
 import numpy as np
 
 GGUF_ALIGN = 32
-T_F32, T_Q8_0 = 0, 8  # GGUF tensor type ids (src/gguf.cpp:378-393)
+T_F32, T_F16, T_Q8_0 = 0, 1, 8  # GGUF tensor type ids (src/gguf.cpp:378-393)
 KV_U32, KV_F32, KV_STRING, KV_ARRAY = 4, 6, 8, 9
 
 QWEN2_05B = dict(n_vocab=151936, n_embd=896, n_layer=24, n_head=14, n_head_kv=2, n_ff=4864,
@@ -86,12 +88,18 @@ def prompt_ids(seed, n, n_vocab):
 
 
 def tensor_plan(hp):
-    """(name, ne, gguf type, init) in file order; init is 'normal' or 'ones'."""
+    """(name, ne, gguf type, init) in file order; init is 'normal' or 'ones'.
+    hp may carry embd_type (T_Q8_0 default, T_F16 or T_F32) for token_embd;
+    with a non-Q8_0 embedding a separate Q8_0 output.weight (the lm_head) is
+    written after it (src/model_qwen2.cpp:497-505)."""
     E, F = hp["n_embd"], hp["n_ff"]
     hd = E // hp["n_head"]
     kv = hd * hp["n_head_kv"]
-    plan = [("token_embd.weight", (E, hp["n_vocab"]), T_Q8_0, "normal"),
+    et = hp.get("embd_type", T_Q8_0)
+    plan = [("token_embd.weight", (E, hp["n_vocab"]), et, "normal"),
             ("output_norm.weight", (E,), T_F32, "ones")]
+    if et != T_Q8_0:
+        plan.append(("output.weight", (E, hp["n_vocab"]), T_Q8_0, "normal"))
     for l in range(hp["n_layer"]):
         b = f"blk.{l}."
         plan += [(b + "attn_norm.weight", (E,), T_F32, "ones"),
@@ -111,7 +119,7 @@ def tensor_plan(hp):
 
 def _nbytes(ne, t):
     n = int(np.prod(ne))
-    return n * 4 if t == T_F32 else n // 32 * 34
+    return n * 4 if t == T_F32 else (n * 2 if t == T_F16 else n // 32 * 34)
 
 
 def _str(s):
@@ -170,7 +178,12 @@ def write_qwen2_q8_0(path, seed, hp=None, chunk=1 << 22):
                 step = chunk - chunk % 32
                 for s in range(0, n, step):
                     x = normal_chunk(seed, ti, s, min(step, n - s))
-                    put((quantize_q8_0(x) if t == T_Q8_0 else x).tobytes())
+                    if t == T_Q8_0:
+                        put(quantize_q8_0(x).tobytes())
+                    elif t == T_F16:
+                        put(x.astype(np.float16).tobytes())
+                    else:
+                        put(x.tobytes())
             nb = _nbytes(ne, t)
             pad = _align(pos + nb) - (pos + nb)
             put(b"\0" * pad)

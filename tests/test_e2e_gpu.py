@@ -161,3 +161,29 @@ def test_tiny_incremental_prefill_equals_batched_bitwise(tiny):
             _, step = m.forward([t], n_past=i, want_logits=True)
         assert np.array_equal(bits(np.frombuffer(batched, dtype=np.float32)),
                               bits(np.frombuffer(step, dtype=np.float32)))
+
+
+@pytest.mark.parametrize("embd_type", [gg.T_F16, gg.T_F32])
+def test_tiny_model_unquantised_embedding_with_separate_lm_head(tmp_path, embd_type):
+    # token_embd in F16 / F32 (the embedding lookup's other types) and a separate
+    # Q8_0 output.weight as the lm_head: bit-identical to the reference engine
+    if not os.path.exists(MINI_INFER):
+        pytest.skip("oracle/_ref/mini_infer is not built")
+    hp = dict(TINY, n_layer=2, embd_type=embd_type)
+    path = str(tmp_path / "m.gguf")
+    gg.write_qwen2_q8_0(path, 13, hp)
+    prompt = gg.prompt_ids(13, 19, hp["n_vocab"])
+    (tmp_path / "ids.txt").write_text(" ".join(map(str, prompt)))
+    dump = tmp_path / "dump"
+    dump.mkdir()
+    subprocess.run([MINI_INFER, path, "--prompt-ids", str(tmp_path / "ids.txt"), "-c", "64", "--dump",
+                    str(dump)], capture_output=True, timeout=60, check=True)
+    r = subprocess.run([MINI_INFER, path, "--prompt-ids", str(tmp_path / "ids.txt"), "-c", "64", "-n", "12",
+                        "-t", "4"], capture_output=True, text=True, timeout=60, check=True)
+    want = np.fromfile(dump / "logits.bin", dtype=np.float32).reshape(len(prompt), -1)
+    with Qwen2(path, n_ctx=64, max_tokens=len(prompt)) as m:
+        m.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
+        _, logits = m.forward(prompt, n_past=0, last_logits_only=False, want_logits=True)
+        got = np.frombuffer(logits, dtype=np.float32).reshape(len(prompt), -1)
+        assert np.array_equal(bits(got), bits(want))
+        assert m.generate(prompt, 12) == [int(t) for t in r.stdout.split()]
