@@ -75,6 +75,21 @@ struct Q8Quantize {
   int64_t src_nb[4], dst_nb[4];
   int64_t ne0, ne1, ne2, rows;  // rows = ne1 * ne2 * ne3
 };
+// RoPE and the K/V append as the epilogue of the stacked Q/K/V projection
+// (one column): rows are n_q Q rows then n_kv K rows then n_kv V rows, Q and K
+// rows permuted within each head of hd rows so that row 2j holds dim j and row
+// 2j + 1 dim j + hd/2 (a rotation pair in one 8-row group). Q lands roped in
+// natural order at q_out, K roped and V as is in the cache rows of position
+// pos (element (head h, dim d) at k_row / v_row + h * c_s1 + 4 d).
+struct RopeEpi {
+  const float* cs;  // (cos, sin) pairs, float2 at [pos * hd/2 + j]
+  float* q_out;
+  char* k_row;
+  char* v_row;
+  int64_t c_s1;
+  int32_t pos, hd, n_q, n_kv;
+};
+
 struct Q8MulMat {
   const char* w;  // n rows of k/32 34-byte blocks, row i at w_nb1 * i
   const char* a;  // m columns of k/32 36-byte blocks, column j at a_nb1 * j
@@ -94,7 +109,22 @@ struct Q8MulMat {
   int64_t x_ld = 0;
   const float* norm_w = nullptr;
   float eps = 0.0f;
+  // Rows of the first perm_rows permuted within heads of perm_hd rows as
+  // RopeEpi describes; the stores put them back in natural order (0: none).
+  int32_t perm_hd = 0;
+  int64_t perm_rows = 0;
+  // With rope_on (streaming form, m = 1): the RopeEpi stores replace dst's.
+  int32_t rope_on = 0;
+  RopeEpi rope{};
 };
+
+// The natural row of stored row r of a matrix whose first perm_rows rows are
+// permuted within heads of hd rows (row 2j <- dim j, 2j + 1 <- dim j + hd/2).
+__host__ __device__ inline int64_t q8_unperm_row(int64_t r, int32_t hd, int64_t perm_rows) {
+  if (hd == 0 || r >= perm_rows) return r;
+  const int64_t head = r / hd, w = r - head * hd;
+  return head * hd + (w >> 1) + (w & 1) * (hd / 2);
+}
 // Whether launch_mul_mat_q8_0 takes the streaming form for p (the only form
 // with the activation prologue).
 bool q8_ring_form(const Q8MulMat& p);

@@ -104,7 +104,7 @@ __global__ __launch_bounds__(256) void mul_mat_q8_0_kernel(const Q8MulMat p) {
         s = s + __shfl_xor(s, 2, 8);
         if (live && l == 0) {
           if (p.add) s = s + gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1);
-          gstore<float>(p.dst + row * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
+          gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
         }
       }
     }
@@ -138,7 +138,10 @@ __device__ inline unsigned lds_take(__attribute__((address_space(3))) unsigned* 
   return t;
 }
 
-template <int M>
+// EPI: the stacked Q/K/V epilogue (rows permuted within heads; RoPE and the
+// K/V append for one column) -- a separate instantiation, so the plain form
+// carries none of it.
+template <int M, bool EPI>
 __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel(const Q8MulMat p) {
 #pragma clang fp contract(off)
   extern __shared__ __attribute__((aligned(16))) char ring_lds[];
@@ -270,12 +273,41 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
         if (row < p.n && l == 0) acc[c] = acc[c] + gload<float>(p.add + row * p.add_nb0 + c * p.add_nb1);
       wait_vmem<0>();
     }
+    // RoPE epilogue (one column): the rotation partner is row rs ^ 1 of this
+    // group, 8 lanes away; the destination is chosen per lane, so it is still
+    // one store instruction
+    float* dst_rope = nullptr;
+    if constexpr (EPI && M == 1) {
+      if (p.rope_on) {
+        const RopeEpi& re = p.rope;
+        const float other = __shfl_xor(acc[0], 8);
+        const int64_t qk_rows = (int64_t)re.n_q + re.n_kv;
+        const int64_t h = row / re.hd;  // head (Q heads, then K heads, then V heads)
+        const int w = (int)(row - h * re.hd);
+        if (row < qk_rows) {
+          const float2 cs = *reinterpret_cast<const float2*>(re.cs + 2 * ((int64_t)re.pos * (re.hd / 2) + (w >> 1)));
+          const float x0 = (w & 1) ? other : acc[0], x1 = (w & 1) ? acc[0] : other;
+          acc[0] = (w & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+        }
+        const int d = row < qk_rows ? (w >> 1) + (w & 1) * (re.hd / 2) : w;
+        if (row < re.n_q)
+          dst_rope = re.q_out + h * re.hd + d;
+        else if (row < qk_rows)
+          dst_rope = reinterpret_cast<float*>(re.k_row + (h - re.n_q / re.hd) * re.c_s1) + d;
+        else
+          dst_rope = reinterpret_cast<float*>(re.v_row + (h - qk_rows / re.hd) * re.c_s1) + d;
+      }
+    }
     // the slot's reads are done before it is refilled; then M stores (row 0
     // of a group always exists, so every store instruction issues), 8 loads
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int c = 0; c < M; ++c)
-      if (row < p.n && l == 0) gstore<float>(p.dst + row * p.dst_nb0 + c * p.dst_nb1, acc[c]);
+    for (int c = 0; c < M; ++c) {
+      float* const o = !EPI ? reinterpret_cast<float*>(p.dst + row * p.dst_nb0 + c * p.dst_nb1)
+                       : dst_rope ? dst_rope
+                                  : reinterpret_cast<float*>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + c * p.dst_nb1);
+      if (row < p.n && l == 0) gstore<float>(o, acc[c]);
+    }
     const int64_t gn = refill(s);
     if (s)
       g_1 = gn;
@@ -398,7 +430,7 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
         s = s + __shfl_xor(s, 2, 8);
         if (live && l == 0) {
           if (p.add) s = s + gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1);
-          gstore<float>(p.dst + row * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
+          gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
         }
       }
     }
@@ -428,31 +460,27 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) 
   const bool rows_form = q8_ring_form(p);
   if (p.x && !rows_form) return hipErrorInvalidValue;  // the prologue exists in the streaming form only
   if (rows_form) {
+    typedef void (*ring_fn)(const Q8MulMat);
+    static const ring_fn fns[2][kQ8Cols] = {
+        {mul_mat_q8_0_ring_kernel<1, false>, mul_mat_q8_0_ring_kernel<2, false>, mul_mat_q8_0_ring_kernel<3, false>,
+         mul_mat_q8_0_ring_kernel<4, false>, mul_mat_q8_0_ring_kernel<5, false>, mul_mat_q8_0_ring_kernel<6, false>,
+         mul_mat_q8_0_ring_kernel<7, false>, mul_mat_q8_0_ring_kernel<8, false>},
+        {mul_mat_q8_0_ring_kernel<1, true>, mul_mat_q8_0_ring_kernel<2, true>, mul_mat_q8_0_ring_kernel<3, true>,
+         mul_mat_q8_0_ring_kernel<4, true>, mul_mat_q8_0_ring_kernel<5, true>, mul_mat_q8_0_ring_kernel<6, true>,
+         mul_mat_q8_0_ring_kernel<7, true>, mul_mat_q8_0_ring_kernel<8, true>}};
     static const hipError_t attr = [] {
       hipError_t e = hipSuccess;
-      const void* fns[kQ8Cols] = {
-          (const void*)&mul_mat_q8_0_ring_kernel<1>, (const void*)&mul_mat_q8_0_ring_kernel<2>,
-          (const void*)&mul_mat_q8_0_ring_kernel<3>, (const void*)&mul_mat_q8_0_ring_kernel<4>,
-          (const void*)&mul_mat_q8_0_ring_kernel<5>, (const void*)&mul_mat_q8_0_ring_kernel<6>,
-          (const void*)&mul_mat_q8_0_ring_kernel<7>, (const void*)&mul_mat_q8_0_ring_kernel<8>};
-      for (const void* f : fns)
-        if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kQ8RingLds);
+      for (int v = 0; v < 2; ++v)
+        for (int m = 0; m < kQ8Cols; ++m)
+          if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)fns[v][m], hipFuncAttributeMaxDynamicSharedMemorySize, kQ8RingLds);
       return e;
     }();
     if (attr != hipSuccess) return attr;
     const int64_t groups = (p.n + 7) / 8;
     const unsigned grid = (unsigned)std::min<int64_t>(n_cu > 0 ? n_cu : 256, (groups + kQ8RingWaves - 1) / kQ8RingWaves);
-    const dim3 bs(kQ8RingWaves * kWave);
-    switch (p.m) {
-      case 1: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<1>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      case 2: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<2>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      case 3: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<3>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      case 4: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<4>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      case 5: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<5>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      case 6: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<6>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      case 7: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<7>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-      default: hipLaunchKernelGGL(mul_mat_q8_0_ring_kernel<8>, dim3(grid), bs, kQ8RingLds, stream, p); break;
-    }
+    const bool epi = p.rope_on || p.perm_hd;
+    hipLaunchKernelGGL(fns[epi ? 1 : 0][p.m - 1], dim3(grid), dim3(kQ8RingWaves * kWave), kQ8RingLds, stream, p);
   } else if (q8_stage_lds_bytes(p.w_nb1, p.k) <= kQ8StageLdsMax &&
              reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && (8 * p.w_nb1) % 16 == 0 &&
              p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0) {

@@ -284,9 +284,14 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   m->row_e = E / 32 * 34;
   m->row_f = F / 32 * 34;
 
-  // weights: collect (source, bytes) pieces in device order
+  // weights: collect (source, bytes) pieces in device order. The stacked Q
+  // and K rows (and their biases) are permuted within each head so that a
+  // RoPE pair, dims j and j + head_dim/2, are adjacent rows (2j, 2j + 1): the
+  // matrix kernel's epilogue then rotates them in place; staged in host
+  // memory, one copy per matrix.
   struct Piece { const uint8_t* src; size_t bytes; size_t off; };
   std::vector<Piece> pieces;
+  std::vector<std::vector<uint8_t>> staged;
   size_t off = 0;
   auto place = [&](std::initializer_list<const mi::GgufTensor*> ts) {
     const size_t start = off;
@@ -295,6 +300,24 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
       off += t->nbytes;
     }
     off = mi::align256(off);
+    return start;
+  };
+  auto place_rope_rows = [&](std::initializer_list<const mi::GgufTensor*> ts, int64_t perm_rows, size_t rb) {
+    size_t total = 0;
+    for (const mi::GgufTensor* t : ts) total += t->nbytes;
+    std::vector<uint8_t> buf(total);
+    size_t o = 0;
+    for (const mi::GgufTensor* t : ts) {
+      std::memcpy(buf.data() + o, t->data, t->nbytes);
+      o += t->nbytes;
+    }
+    std::vector<uint8_t> out(buf);  // rows of rb bytes (a weight row, or one bias element)
+    for (int64_t r = 0; r < perm_rows; ++r)
+      std::memcpy(out.data() + r * rb, buf.data() + mi::q8_unperm_row(r, hd, perm_rows) * rb, rb);
+    staged.push_back(std::move(out));
+    const size_t start = off;
+    pieces.push_back({staged.back().data(), total, off});
+    off = mi::align256(off + total);
     return start;
   };
   const mi::GgufTensor *on, *ow = nullptr;
@@ -326,8 +349,9 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
         (rc = check_tensor(f, b + "ffn_up.weight", mi::kGgufTQ8_0, E, F, &wu)) ||
         (rc = check_tensor(f, b + "ffn_down.weight", mi::kGgufTQ8_0, F, E, &wd)))
       return rc;
-    lo[l] = {place({an}), place({wq, wk, wv}), place({bq, bk, bv}), place({wo}), place({fn}),
-             place({wg, wu}), place({wd})};
+    lo[l] = {place({an}), place_rope_rows({wq, wk, wv}, E + m->kvd, (size_t)m->row_e),
+             place_rope_rows({bq, bk, bv}, E + m->kvd, sizeof(float)),
+             place({wo}), place({fn}), place({wg, wu}), place({wd})};
   }
   // everything above is host-side validation; the device is touched from here on
   if ((rc = mi::rt_bind())) return rc;
@@ -413,7 +437,8 @@ int quantize_cols(const mi_hip_qwen2* m, const float* src, int64_t ne0, int64_t 
 // streaming matrix kernel with the norm / quantisation as its prologue (one
 // launch); the others run the norm or quantize kernel into m->aq first.
 int proj(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, int64_t k, Act act,
-         int64_t m_cols, float* dst, int64_t dst_ld, const float* add, int64_t add_ld) {
+         int64_t m_cols, float* dst, int64_t dst_ld, const float* add, int64_t add_ld,
+         const mi::RopeEpi* rope = nullptr, bool* roped = nullptr) {
   mi::Q8MulMat p{};
   p.w = w;
   p.a = m->aq;
@@ -445,6 +470,18 @@ int proj(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, int
         if (rc) return rc;
       }
     }
+  }
+  if (rope) {
+    // the stacked Q/K rows are stored permuted: rotated in the epilogue when
+    // the streaming form runs a single column, else put back in natural order
+    if (p.x && m_cols == 1 && mi::q8_ring_form(p)) {
+      p.rope_on = 1;
+      p.rope = *rope;
+    } else {
+      p.perm_hd = rope->hd;
+      p.perm_rows = (int64_t)rope->n_q + rope->n_kv;
+    }
+    if (roped) *roped = p.rope_on != 0;
   }
   hipError_t e = mi::launch_mul_mat_q8_0(p, mi::rt_n_cu(), m->stream);
   return e == hipSuccess ? MI_HIP_OK : mi::rt_hip_fail(e, "qwen2 mul_mat launch");
@@ -484,10 +521,28 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
   const float scale = 1.0f / std::sqrt((float)hd);
   for (int l = 0; l < hp.n_layer; ++l) {
     const mi_hip_qwen2::Layer& w = m->layers[l];
-    if ((rc = proj(m, w.wqkv, m->row_e, qkv_rows, E, {m->x, w.attn_norm}, T, m->qkv, qkv_rows, w.bqkv, 0)))
-      return rc;
     const size_t nb[3] = {4, 4 * (size_t)hd, 4 * (size_t)qkv_rows};
-    {
+    void* kc = nullptr;
+    void* vc = nullptr;
+    int64_t cne[4];
+    size_t cnb[4];
+    if ((rc = mi_hip_kv_view(m->kv, l, 0, &kc, cne, cnb)) || (rc = mi_hip_kv_view(m->kv, l, 1, &vc, cne, cnb)))
+      return rc;
+    mi::RopeEpi re{};
+    re.cs = m->rope_cs;
+    re.q_out = m->qkv;
+    re.k_row = static_cast<char*>(kc) + (int64_t)n_past * (int64_t)cnb[2];
+    re.v_row = static_cast<char*>(vc) + (int64_t)n_past * (int64_t)cnb[2];
+    re.c_s1 = (int64_t)cnb[1];
+    re.pos = n_past;
+    re.hd = hd;
+    re.n_q = E;
+    re.n_kv = m->kvd;
+    bool roped = false;
+    if ((rc = proj(m, w.wqkv, m->row_e, qkv_rows, E, {m->x, w.attn_norm}, T, m->qkv, qkv_rows, w.bqkv, 0, &re,
+                   &roped)))
+      return rc;
+    if (!roped) {
       // RoPE on Q and K in place, K and V appended at positions n_past.. (one launch)
       mi::RopeAppend ra{};
       ra.q = reinterpret_cast<const char*>(m->qkv);
