@@ -21,6 +21,8 @@ import argparse
 import ctypes
 import json
 import os
+import re
+import subprocess
 import sys
 import time
 
@@ -41,7 +43,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,prefill,d7b,perlayer,q8,e2e,copy (copy: the "
+                    help="comma list: decode,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
                          "counter calibration workload, only when named)")
     return ap.parse_args()
 
@@ -199,6 +201,48 @@ def bench_copy(torch, steps, warmup, nbytes=256 << 20):
     dst = torch.empty_like(src)
     kern_ms = run_timed(torch, lambda i: dst.copy_(src), steps, warmup)
     return dict(bytes=nbytes, kernel_ms=kern_ms, gbps=2 * nbytes / (kern_ms * 1e-3) / 1e9)
+
+
+def device_info():
+    """CU count and peak engine clock of the gfx950 agent as rocminfo reports
+    them (None where rocminfo is absent)."""
+    info = {"cus": None, "max_clock_mhz": None}
+    try:
+        txt = subprocess.run(["/opt/rocm/bin/rocminfo"], capture_output=True, text=True,
+                             timeout=60).stdout
+    except (OSError, subprocess.SubprocessError):
+        return info
+    for agent in txt.split("Agent ")[1:]:
+        if "gfx950" not in agent:
+            continue
+        cu = re.search(r"Compute Unit:\s+(\d+)", agent)
+        clk = re.search(r"Max Clock Freq\. \(MHz\):\s+(\d+)", agent)
+        info["cus"] = int(cu.group(1)) if cu else None
+        info["max_clock_mhz"] = int(clk.group(1)) if clk else None
+        break
+    return info
+
+
+def bench_memread(torch, lib, stream, steps, warmup, nbytes=1 << 30,
+                  shapes=(1024, 2048, 4096, 8192, 16384)):
+    """The measured read-bandwidth ceiling (mi_hip_memread, the device
+    counterpart of tools/bench_memread.cpp): a load-and-accumulate pass over
+    1 GiB (4x the 256 MB MALL), back to back, at several workgroup counts;
+    the fastest is the ceiling."""
+    src = torch.empty(nbytes // 4, device="cuda").uniform_()
+    sums = torch.empty(max(shapes), device="cuda")
+    a, s = ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(sums.data_ptr())
+    per = {}
+    for n in shapes:
+        ms = run_timed(torch, lambda i: lib.check(lib.mi_hip_memread(a, nbytes, s, n, stream)),
+                       steps, warmup)
+        torch.cuda.synchronize()
+        total = float(sums[:n].double().sum().item())
+        assert abs(total / (nbytes // 4) - 0.5) < 0.01, "read pass sums disagree with the buffer"
+        per[n] = nbytes / (ms * 1e-3) / 1e9
+    best = max(per, key=per.get)
+    return dict(bytes=nbytes, n_sums=best, gbps=per[best],
+                gbps_by_workgroups={str(k): round(v, 1) for k, v in per.items()})
 
 
 E2E_SEED = 1234
@@ -379,6 +423,14 @@ def main():
         import shutil
         shutil.rmtree(e2e_dir, ignore_errors=True)
 
+    if want("memread"):
+        res["memread"] = bench_memread(torch, lib, stream, 20, 3)
+        res["memread"].update(device_info())
+        print(f"# read ceiling 1 GiB: {res['memread']['gbps']:.1f} GB/s "
+              f"(by workgroup count: {res['memread']['gbps_by_workgroups']}); rocminfo: "
+              f"{res['memread']['cus']} CUs, {res['memread']['max_clock_mhz']} MHz", file=sys.stderr,
+              flush=True)
+
     if "copy" in only:
         res["copy"] = bench_copy(torch, max(5, args.steps // 10), 2)
         print(f"# copy 256 MiB: {res['copy']['gbps']:.1f} GB/s (read + write)", file=sys.stderr,
@@ -420,6 +472,14 @@ def main():
             "traffic": measured_traffic(),
             "bytes_per_launch": d["bytes"], "kernel_us": round(d["kernel_ms"] * 1e3, 3),
         }
+        if "memread" in res:
+            m = res["memread"]
+            out["roofline"]["measured_read_ceiling"] = {
+                "gbps": round(m["gbps"], 1), "frac_of_peak": round(m["gbps"] / HBM_PEAK_GBPS, 4),
+                "achieved_frac_of_ceiling": round(d["kernel_gbps"] / m["gbps"], 4),
+                "workload": f"mi_hip_memread: load-and-accumulate pass over 1 GiB, {m['n_sums']} "
+                            "workgroups of 512 (the fastest of 1024-16384)",
+                "cus": m["cus"], "max_clock_mhz": m["max_clock_mhz"]}
     if cpu:
         out["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                for k, v in cpu.items()}

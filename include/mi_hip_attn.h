@@ -260,6 +260,18 @@ int mi_hip_graph_prepare(const mi_cgraph* graph);
  * chain (no-ops); ATTN_KQV of a planned fused chain (the fused launch). */
 int mi_hip_compute_forward(mi_tensor* dst, int ith, int nth);
 
+/* ---- read-bandwidth ceiling ---------------------------------------------- */
+
+/* The device counterpart of tools/bench_memread.cpp (the engine's read-only
+ * bandwidth ceiling: a load-and-accumulate pass, one reduced sum per worker,
+ * no writes to the source): n_sums workgroups each sum one contiguous slice
+ * of src[0, bytes) (float data) and write sums[w]; sum(sums) is the sum of
+ * the buffer up to float rounding. src is device memory, 16-byte aligned,
+ * bytes a multiple of 16; sums is device memory of n_sums floats, 1 <= n_sums
+ * <= 65536. Timed by the caller on `stream`: bytes / kernel time is the
+ * measured ceiling that the decode kernels are compared with. */
+int mi_hip_memread(const void* src, size_t bytes, float* sums, int32_t n_sums, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -155,6 +155,9 @@ hipError_t launch_attn_exact(const ExactAttn& p, hipStream_t stream);
 // Host helpers of the library's entry points (runtime.hip), for the other
 // host files: the thread's last-error message, the accounted device
 // allocator, selecting the library's device, and its compute-unit count.
+// The read-bandwidth ceiling pass (memread.hip): n_sums workgroups, one float each.
+hipError_t launch_memread(const void* src, size_t bytes, float* sums, int n_sums, hipStream_t stream);
+
 int rt_fail(int code, const char* msg);
 int rt_hip_fail(hipError_t e, const char* what);
 int rt_alloc(void** p, size_t bytes, const char* what);

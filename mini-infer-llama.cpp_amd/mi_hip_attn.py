@@ -166,6 +166,7 @@ SIGNATURES = {
     "mi_hip_op_quantize_q8_0": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_op_mul_mat": ([ctypes.POINTER(MiTensor), _P], _I),
     "mi_hip_rope_append": ([ctypes.POINTER(RopeArgs)], _I),
+    "mi_hip_memread": ([_P, ctypes.c_size_t, _P, ctypes.c_int32, _P], _I),
     "mi_hip_graph_prepare": ([ctypes.POINTER(MiCgraph)], _I),
     "mi_hip_compute_forward": ([ctypes.POINTER(MiTensor), _I, _I], _I),
     "mi_hip_qwen2_load": ([ctypes.c_char_p, ctypes.c_int32, ctypes.c_int32,

@@ -166,3 +166,14 @@ def test_alloc_limit_and_stats(lib):
     assert s.n_malloc >= s.n_free
     assert lib.mi_hip_set_alloc_limit(1 << 20) == 0
     assert lib.mi_hip_set_alloc_limit(0) == 0
+
+
+def test_memread_rejects_bad_arguments_without_device(lib):
+    # argument checks come before any device work (addresses below are never touched)
+    p, s = ctypes.c_void_p(1 << 20), ctypes.c_void_p(2 << 20)
+    assert lib.mi_hip_memread(None, 256, s, 4, None) == 1 and "memread" in lib.last_error()
+    assert lib.mi_hip_memread(p, 0, s, 4, None) == 1
+    assert lib.mi_hip_memread(p, 250, s, 4, None) == 1
+    assert lib.mi_hip_memread(ctypes.c_void_p((1 << 20) + 4), 240, s, 4, None) == 1
+    assert lib.mi_hip_memread(p, 256, s, 0, None) == 1
+    assert lib.mi_hip_memread(p, 256, s, 65537, None) == 1 and "n_sums" in lib.last_error()
