@@ -43,6 +43,7 @@ extern "C" {
 #define MI_HIP_E_NOMEM 4       /* device allocation refused (or over the limit) */
 #define MI_HIP_E_UNSUPPORTED 5 /* valid request outside what the kernels cover */
 #define MI_HIP_E_STATE 6       /* called before mi_hip_init / on a dead object */
+#define MI_HIP_E_LOST 7        /* a decode launch lost a record (its group's output is NaN) */
 
 /* ---- library lifetime -------------------------------------------------- */
 
@@ -51,8 +52,8 @@ extern "C" {
  * (src/model_qwen2.cpp:557-596); idempotent for the same device. */
 int mi_hip_init(int device);
 
-/* Releases library-owned device memory (workspace). KV caches must have been
- * destroyed by the caller first. */
+/* Releases library-owned device memory (the default workspace). KV caches
+ * and workspaces must have been destroyed by the caller first. */
 int mi_hip_shutdown(void);
 
 /* Thread-local text of the last failure ("" if none). */
@@ -81,6 +82,56 @@ int mi_hip_get_alloc_stats(mi_hip_alloc_stats* out);
  * would exceed the cap fails with MI_HIP_E_NOMEM before calling HIP. */
 int mi_hip_set_alloc_limit(uint64_t bytes);
 
+/* ---- decode workspace ---------------------------------------------------- */
+
+/* The split-KV decode kernel's scratch: one partial-result record per
+ * workgroup, per-group counters (dynamic sub-tile claims, merge election,
+ * arrivals) and status words. Launches that share a workspace must be
+ * ordered (one stream, or synchronised); launches on different workspaces may
+ * run concurrently. Every KV cache owns one (mi_hip_kv_workspace); callers
+ * that attend over explicit tensors create their own, or fall back to the
+ * library's default workspace (created by mi_hip_init, shared by every call
+ * that names none). No counterpart in the reference: its CPU kernels need no
+ * scratch beyond the graph allocator's arena (src/gallocr.cpp). */
+typedef struct mi_hip_workspace mi_hip_workspace;
+
+typedef struct mi_hip_workspace_desc {
+  int32_t n_head_kv;  /* KV heads of the problems it serves */
+  int32_t n_head;     /* Q heads (multiple of n_head_kv) */
+  int32_t head_dim;   /* 64 or 128 */
+} mi_hip_workspace_desc;
+
+/* One device allocation covering any decode launch of up to 32 items of this
+ * head shape (mi_hip_attn_decode_batch's limit per launch). */
+int mi_hip_workspace_create(const mi_hip_workspace_desc* desc, mi_hip_workspace** out);
+int mi_hip_workspace_destroy(mi_hip_workspace* ws);
+
+typedef struct mi_hip_workspace_status {
+  uint32_t early_fallbacks; /* early merges whose bounded wait ran out (results still exact) */
+  uint32_t lost_groups;     /* groups whose output was set to NaN (never expected) */
+} mi_hip_workspace_status;
+
+/* Synchronises `stream`, reports the status words accumulated since the last
+ * call and clears them. Returns MI_HIP_E_LOST if any group was lost (its
+ * counters are then reset too), MI_HIP_OK otherwise. */
+int mi_hip_workspace_check(mi_hip_workspace* ws, void* stream, mi_hip_workspace_status* out);
+
+/* Rounds of polls an early merger makes before it falls back to the
+ * last-arriver merge (default 4096). Tuning and tests; 0 makes every early
+ * merge fall back. */
+int mi_hip_workspace_set_poll_limit(mi_hip_workspace* ws, int32_t rounds);
+
+/* Decode planner knobs (initialised from MI_HIP_DECODE_KPG, _EARLY, _SOLO and
+ * _CLAIM at mi_hip_init): kpg > 0 forces that many workgroups per group (0:
+ * planned); early = 0 disables the early merge, 1 uses it when every
+ * workgroup of a launch fits on the device at once, 2 always; solo: groups
+ * that one workgroup's ring covers in at most `solo` rounds get one
+ * workgroup; claim: split groups whose waves each stream at least `claim`
+ * ring rounds take sub-tiles from device counters (0: never). A negative
+ * value keeps the current setting. Tuning and tests; no counterpart in the
+ * reference. */
+int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim);
+
 /* ---- device-resident KV cache ------------------------------------------ */
 
 typedef struct mi_hip_kv mi_hip_kv;
@@ -97,12 +148,14 @@ typedef struct mi_hip_kv_desc {
 /* One device allocation holding every layer's K and V as
  * [head_dim, n_head_kv, n_ctx] (position-major, the layout of
  * src/model_qwen2.cpp:564-577), plus the host-node staging buffer (sized for
- * n_ctx) and the library's split-KV workspace (grown, if needed, to cover a
- * decode launch of up to 32 items of this head shape). Nothing is allocated
- * afterwards.
+ * n_ctx) and the cache's own decode workspace (covering a decode launch of up
+ * to 32 items of this head shape). Nothing is allocated afterwards.
  * Replaces mi_kv_cache_init's host KV context (src/model_qwen2.cpp:564-577). */
 int mi_hip_kv_create(const mi_hip_kv_desc* desc, mi_hip_kv** out);
 int mi_hip_kv_destroy(mi_hip_kv* kv);
+
+/* The cache's own decode workspace (owned by the cache; do not destroy). */
+int mi_hip_kv_workspace(mi_hip_kv* kv, mi_hip_workspace** out);
 
 /* Device view of one layer's cache: which = 0 for K, 1 for V. Fills the
  * device address and the engine-style ne[4]/nb[4]. */
@@ -153,6 +206,9 @@ typedef struct mi_hip_attn_args {
   int32_t n_tokens; /* 1 = decode kernel, > 1 = prefill kernel */
   float scale;      /* op_params[1] of SOFTMAX, 1/sqrt(head_dim) in the engine */
   void* stream;
+  /* Decode scratch: this workspace if non-NULL, else kv's own, else the
+   * library default (read from the first item of a batch). */
+  mi_hip_workspace* ws;
 } mi_hip_attn_args;
 
 /* The whole ATTN_QK -> causal SOFTMAX -> ATTN_KQV triple in one pass that

@@ -34,24 +34,47 @@ struct DecodeItem {
   int32_t kpg;         // workgroups per group
 };
 
+// Per-group counter block of the decode workspace (kCtrInts words, 256 bytes,
+// so groups never share a cache line): the dynamic sub-tile claims, the early
+// protocol's merger election, start count (plus the merger's give-up mark),
+// late-part count and give-up point, and the team arrivals.
+constexpr int kCtrInts = 64;
+constexpr int kCtrClaim = 0;
+constexpr int kCtrElect = 16;
+constexpr int kCtrStarted = 17;
+constexpr int kCtrLate = 18;
+constexpr int kCtrGaveUpAt = 19;
+constexpr int kCtrTeams = 32;  // team t arrives at word kCtrTeams + t (t < 32)
+// Status words of a workspace: [0] early merges whose bounded wait ran out and
+// that fell back to the last-arriver merge; [1] records never seen (the output
+// of that group is NaN). Cleared by the host.
+constexpr int kStatusWords = 4;
+
 // Work decomposition. A group is (item, KV head g, head chunk hc): the G Q
 // heads g*n_rep + hc*G .. + G - 1 that read KV head g. Each group is served by
-// kpg workgroups of its item; workgroup wg0 + gl*kpg + part owns positions
-// [n_kv*part/kpg, n_kv*(part+1)/kpg) of the item's group gl and leaves one
-// record when kpg > 1.
+// kpg workgroups of its item (workgroups wg0 + gl*kpg + part, part < kpg),
+// which take the group's 16-position sub-tiles dynamically and leave one
+// record each when kpg > 1.
 struct DecodeParams {
-  DecodeItem item[kDecodeMaxItems];
+  // Scalars first: the kernel reads them in one round of scalar loads.
   int32_t n_items;
   int32_t n_rep;        // Q heads per KV head
   int32_t n_head_kv;
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
+  int32_t gpi;          // groups per item, n_head_kv * n_chunks
   int32_t n_wg;         // workgroups
-  int32_t cst;          // arrival counters per group: 1 + teams of its largest item
+  int32_t uniform_kpg;  // > 0: every item has this kpg, so item = wg / (gpi * kpg)
   int32_t early;        // groups of 2..kDecodeEarlyMax workgroups merged by their first finisher
-  uint32_t epoch;       // launch stamp of early records (nonzero, new for every launch)
+  int32_t max_polls;    // the early merger's bounded wait (rounds of polls) before it falls back
+  int32_t ctr_groups;   // groups one counter set covers
+  int32_t clear_groups; // groups [0, clear_groups) of the other counter set to clear
+  uint32_t epoch;       // launch stamp (nonzero, new for every launch on this workspace)
   float scale_log2e;    // softmax scale * log2(e)
   float* rec;           // one record per workgroup
-  unsigned* cnt;        // cst arrival counters per (item, group); zero between launches
+  unsigned* cnt;        // two counter sets of ctr_groups * kCtrInts words: launch e uses set
+                        // e & 1 (zero on entry) and clears set (e + 1) & 1 for the next launch
+  unsigned* status;     // kStatusWords status words
+  DecodeItem item[kDecodeMaxItems];
 };
 
 // ---------------------------------------------------------------------------

@@ -6,20 +6,28 @@
 // Work decomposition. A group is (item, KV head g, head chunk hc): the G <= 4*HS
 // Q heads that read KV head g (GQA is an index mapping: every K/V row is read
 // once for all G heads, never copied). Each group is served by kpg workgroups
-// (the host sizes kpg so the launch has about one workgroup per CU); workgroup
-// part p owns the contiguous share [n_kv p / kpg, n_kv (p + 1) / kpg) of the
-// group's positions, cut into sub-tiles of 16 positions (the last one
-// partial) that its NWV waves take one at a time from an LDS counter, so the
-// waves finish together however unevenly memory serves them. A workgroup
-// never changes group, so its waves never meet before the end.
+// (the host sizes kpg so the launch has about one workgroup per CU). The
+// group's positions are cut into sub-tiles of 16 (the last one partial) that
+// the waves of its workgroups take one at a time:
+//   - claims (groups long enough that each wave streams several ring
+//     cycles): each wave's first NB sub-tiles are fixed (a prefix of the
+//     group spread over its workgroups); every refill then claims one more
+//     sub-tile from the group's counter in device memory. The claim is issued
+//     a whole ring cycle before its result is used, so its latency hides
+//     behind the loads in flight, and the workgroups of a group finish
+//     together however unevenly the memory system serves them;
+//   - local takes (short groups, where a claim's round trip would not hide):
+//     part p of the group's kpg workgroups owns sub-tiles p, p + kpg,
+//     p + 2 kpg, ..., and its waves take them in turn from an LDS counter.
 //
 // Streaming. Each wave owns an LDS ring of NB slots; a slot holds one
 // sub-tile's K rows then its V rows, written by buffer_load ... lds (direct to
-// LDS, no registers). Every refill is issued -- past the share's last
-// sub-tile through a zero-sized resource that reads nothing -- so the number of loads
-// issued after any slot's K (or V) is always the same and the waits are fixed
-// vmcnt values. Rows past the share lie outside the sub-tile's bounded
-// resource and arrive as zeros without a memory request. The 16-byte slots of each K row are stored XOR-swizzled by
+// LDS, no registers). Every slot is refilled once per ring cycle, with a
+// zero-sized resource that reads nothing once the wave has run out of
+// sub-tiles, so the number of memory operations issued after any slot's K (or
+// V) is always the same and the waits are fixed vmcnt values. Rows past n_kv
+// lie outside the sub-tile's bounded resource and arrive as zeros without a
+// memory request. The 16-byte slots of each K row are stored XOR-swizzled by
 // row, so the lane-per-row reads below are free of bank conflicts.
 //
 // Per sub-tile (lane = (row r = lane / 16, column i = lane % 16)):
@@ -32,28 +40,30 @@
 //       come back as a broadcast read.
 //
 // Combining. At the end the waves' (m, l, acc) meet in LDS. With kpg == 1 the
-// workgroup writes O. Otherwise it writes one record (agent-scope atomic
-// stores, which bypass the non-coherent L2) and bumps its team's arrival
-// counter (a team: up to as many workgroups as one merge round reads); the
-// workgroup that arrives last reads the team's records (agent-scope atomic
-// loads) and merges them with the stable rescaling
-// O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s. With one team it writes
-// O; otherwise the team result becomes a record again and the last team
-// merges the team records the same way. Every merger re-arms its counter.
-// Ordering without fences: each wave waits for its record stores (vmcnt 0)
-// before the workgroup barrier that precedes the counter increment, and the
-// reader issues its loads only after the increment returned. (A device-scope
-// fence would write back and invalidate the XCD's whole L2 instead.)
-//
-// Early combining, for groups of 2..kDecodeEarlyMax workgroups when every
-// workgroup of the launch is resident at once (the host sets p.early): the
-// group's first workgroup to finish claims the merge with one atomic (issued
-// while its waves deposit); the others store their record as 64-bit (value,
-// launch epoch) words and exit, with no acknowledgement wait and no counter.
-// The merger polls the records until every word carries this launch's epoch
-// and merges all parts in part order. Its wait overlaps the other parts'
-// streaming, so after the last part finishes only that part's stores, one
-// poll and the merge remain.
+// workgroup writes O. Otherwise partials are merged across workgroups with the
+// stable rescaling O = sum_s 2^(m_s - M) A_s / sum_s 2^(m_s - M) L_s, in part
+// order, by one of two protocols:
+//   - early (groups of 2..kDecodeEarlyMax workgroups): every part counts
+//     itself in the group's start counter when it starts (the result is read
+//     only at the end, so the round trip hides behind the streaming); part 0
+//     merges, the others store their record as 64-bit (value, launch epoch)
+//     words and exit. The merger polls the records until every word carries
+//     this launch's epoch and merges, so after the last part finishes only
+//     that part's stores, one poll and the merge remain. The wait is bounded:
+//     a merger that runs out of polls marks
+//     the start counter. If every part had started by then, they are all
+//     running and it keeps waiting; otherwise it stores its own record and
+//     exits, and the parts that start after the mark (they see it in their
+//     start count) count themselves again at their end: the last of them
+//     merges. So a group whose parts cannot all be resident at once (other
+//     work holds the CUs) costs time, never correctness, and the fallback is
+//     counted in the workspace's status words;
+//   - teams (larger groups): every workgroup stores its record, waits for the
+//     stores and bumps its team's arrival counter; the last arriver of a team
+//     merges the team's records, and the last team merges the team results.
+// Counters come in two sets: launch e uses set e & 1, which launch e - 1
+// cleared, and clears set (e + 1) & 1 for launch e + 1, so no counter is ever
+// re-armed by a merger that might run before a late increment.
 #include <cstdlib>
 #include <type_traits>
 
@@ -193,7 +203,7 @@ __device__ __forceinline__ void qk4(float (&s)[HS][4 / HS], const float (&q)[HS]
 
 
 
-template <int D, typename KT, int HS, int NWV>
+template <int D, typename KT, int HS, int NWV, bool DYN>
 struct DecodeCfg {
   static constexpr int ELT = (int)sizeof(KT);
   static constexpr int RB = D * ELT;              // bytes per cache row
@@ -202,6 +212,7 @@ struct DecodeCfg {
   static constexpr int SUBB = kDecodeSub * RB;    // bytes of one K (or V) sub-tile
   static constexpr int NDK = SUBB / 1024;         // 1 KB loads per K (or V) sub-tile
   static constexpr int NDMA = 2 * NDK;
+  static constexpr int OPS = NDMA + (DYN ? 1 : 0);  // vector memory operations per refill
   static constexpr int SLOTB = 2 * SUBB;          // ring slot: K rows, then V rows
   // 128 KB of ring per workgroup; 64 KB (two slots per wave) with an F16
   // cache at head_dim 128, measured 8% faster there than four slots (14.9 vs
@@ -235,18 +246,37 @@ struct DecodeCfg {
   static constexpr int L_TMP = L_RING + NB * SLOTB;
   static_assert(L_OWN + NP * 24 <= L_RING + NB * SLOTB, "own partial in wave 0's ring");
   static_assert(NSUB <= 1 || L_TMP + NSUB * NP * 24 <= L_RING + NWV * NB * SLOTB, "merge exchange");
-  // vmcnt allowed while waiting for a slot's K (its V and the later slots may
-  // still be in flight) and for its V.
-  static constexpr int WAIT_K = NDK + NDMA * (NB - 1);
-  static constexpr int WAIT_V = NDMA * (NB - 1);
+  // vmcnt allowed while waiting for a slot's K (its V and the later slots'
+  // refills may still be in flight) and for its V. A refill issues its claim
+  // (dynamic takes) before its loads.
+  static constexpr int WAIT_K = NDK + OPS * (NB - 1);
+  static constexpr int WAIT_V = OPS * (NB - 1);
   static_assert(WAIT_K <= 63, "vmcnt range");
+  // Early protocol: teams of at most 32 (the counter block's team words).
+  static constexpr int TEAM = NSUB * 8;
 };
 
-// One workgroup per CU (the LDS ring fills it): NWV / 4 waves per SIMD.
-template <int D, typename KT, int HS, int NWV>
+// One workgroup per CU at most is assumed only by the early protocol's
+// bounded wait (it stays correct without it); the F16 head_dim-128 variant
+// (64 KB ring) can share a CU. NWV / 4 waves per SIMD.
+template <int D, typename KT, int HS, int NWV, bool DYN>
 __global__ __launch_bounds__(NWV* kWave) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
 void decode_kernel(const DecodeParams p) {
-  typedef DecodeCfg<D, KT, HS, NWV> C;
+  // Every scalar parameter in one round of scalar loads (the empty asm needs
+  // them all in registers at once; the compiler would otherwise load each
+  // near its first use, in dependent rounds).
+  const int a_n_items = p.n_items, a_n_rep = p.n_rep, a_n_head_kv = p.n_head_kv, a_n_chunks = p.n_chunks;
+  const int a_gpi = p.gpi, a_n_wg = p.n_wg, a_uniform_kpg = p.uniform_kpg, a_early = p.early;
+  const int a_max_polls = p.max_polls, a_ctr_groups = p.ctr_groups, a_clear_groups = p.clear_groups;
+  const unsigned a_epoch = p.epoch;
+  const float a_scale_log2e = p.scale_log2e;
+  float* const a_rec = p.rec;
+  unsigned* const a_cnt = p.cnt;
+  unsigned* const a_status = p.status;
+  asm volatile("" ::"s"(a_n_items), "s"(a_n_rep), "s"(a_n_head_kv), "s"(a_n_chunks), "s"(a_gpi), "s"(a_n_wg),
+               "s"(a_uniform_kpg), "s"(a_early), "s"(a_max_polls), "s"(a_ctr_groups), "s"(a_clear_groups),
+               "s"(a_epoch), "s"(a_scale_log2e), "s"(a_rec), "s"(a_cnt), "s"(a_status));
+  typedef DecodeCfg<D, KT, HS, NWV, DYN> C;
   constexpr int HSL = C::HSL, NB = C::NB, NSLOT = C::NSLOT, NE = C::NE;
   constexpr int NACC = 4 / HS;
   constexpr bool F16 = C::ELT == 2;
@@ -257,43 +287,90 @@ void decode_kernel(const DecodeParams p) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;  // QK: position in the sub-tile; PV: column block
   const int hb = lane >> 4;   // head slots hb + 4 h
+  const int wg = blockIdx.x;
 
   // Records: one per workgroup, written and read with agent-coherent (sc1)
-  // 16-byte accesses through this resource.
-  const rsrc_t recr = make_rsrc(p.rec, (unsigned)(p.n_wg * C::REC * 4));
+  // accesses through this resource (team protocol) or 64-bit atomics (early).
+  const rsrc_t recr = make_rsrc(a_rec, (unsigned)(a_n_wg * C::REC * 4));
 
-  // Stage the item table (kernel arguments) in LDS; the whole table is copied
-  // so the loads do not wait for n_items.
+  // This launch's counter set; the groups the previous launch used in the
+  // other set are cleared for the next launch (write-through stores: the next
+  // launch's atomics are performed in memory).
+  const size_t set_words = (size_t)a_ctr_groups * kCtrInts;
+  unsigned* const cset = a_cnt + (size_t)(a_epoch & 1u) * set_words;
   {
+    unsigned* const other = a_cnt + (size_t)((a_epoch + 1u) & 1u) * set_words;
+    for (int b = wg; b < a_clear_groups; b += a_n_wg)
+      if (threadIdx.x < kCtrInts)
+        __hip_atomic_store(other + (size_t)b * kCtrInts + threadIdx.x, 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // This workgroup's item. Uniform launches compute it and read its fields
+  // from the kernel arguments with scalar loads; others stage the item table
+  // in LDS (one parallel round trip) and find the item with one ballot.
+  const lds_t* const tab = lds + C::L_ITEMS;
+  if (!DYN && threadIdx.x == 0) lds_store<unsigned>(lds + C::L_FLAG + 4, 0u);  // LDS take counter
+  int ii;
+  const char* it_k;
+  const char* it_v;
+  const float* it_q;
+  float* it_out;
+  int64_t k_s1, v_s1, q_s1, o_s1;
+  int n_kv, kpg, wg0, ks2, vs2;
+  if (a_uniform_kpg > 0) {
+    if (!DYN) wg_barrier();
+    ii = wg / (a_gpi * a_uniform_kpg);
+    const DecodeItem& it = p.item[ii];
+    it_k = it.k;
+    it_v = it.v;
+    it_q = it.q;
+    it_out = it.out;
+    k_s1 = it.k_s1;
+    v_s1 = it.v_s1;
+    q_s1 = it.q_s1;
+    o_s1 = it.o_s1;
+    n_kv = it.n_kv;
+    kpg = it.kpg;
+    wg0 = it.wg0;
+    ks2 = (int)it.k_s2;
+    vs2 = (int)it.v_s2;
+  } else {
     constexpr int V16 = kDecodeMaxItems * (int)(sizeof(DecodeItem) / 16);
     for (int i = threadIdx.x; i < V16; i += NWV * kWave)
       lds_store<f32x4>(lds + C::L_ITEMS + 16 * i, reinterpret_cast<const f32x4*>(&p.item[0])[i]);
-    if (threadIdx.x == 0) lds_store<unsigned>(lds + C::L_FLAG + 4, 0u);  // sub-tile take counter
     wg_barrier();
-  }
-  const lds_t* const tab = lds + C::L_ITEMS;
-
-  // This workgroup's item: the number of items after the first whose first
-  // workgroup is at or below this one (one LDS read per lane and a ballot).
-  const int wg = blockIdx.x;
-  int ii;
-  {
+    // the number of items after the first whose first workgroup is at or below this one
     const int w0 = item_at(tab, lane & (kDecodeMaxItems - 1)).wg0;
-    ii = __popcll(__ballot(lane >= 1 && lane < p.n_items && wg >= w0));
+    ii = __popcll(__ballot(lane >= 1 && lane < a_n_items && wg >= w0));
+    lds_item_t& it = item_at(tab, ii);
+    it_k = uni(it.k);
+    it_v = uni(it.v);
+    it_q = uni(it.q);
+    it_out = uni(it.out);
+    k_s1 = uni(it.k_s1);
+    v_s1 = uni(it.v_s1);
+    q_s1 = uni(it.q_s1);
+    o_s1 = uni(it.o_s1);
+    n_kv = uni(it.n_kv);
+    kpg = uni(it.kpg);
+    wg0 = uni(it.wg0);
+    ks2 = (int)uni(it.k_s2);
+    vs2 = (int)uni(it.v_s2);
   }
-  lds_item_t& it = item_at(tab, ii);
-  const int n_kv = uni(it.n_kv), kpg = uni(it.kpg);
-  const char* const it_k = uni(it.k);
-  const char* const it_v = uni(it.v);
-  const float* const it_q = uni(it.q);
-  float* const it_out = uni(it.out);
-  const int64_t k_s1 = uni(it.k_s1), v_s1 = uni(it.v_s1), q_s1 = uni(it.q_s1), o_s1 = uni(it.o_s1);
-  const int local = wg - uni(it.wg0);
+  const int local = wg - wg0;
   const int gl = local / kpg, part = local - gl * kpg;
-  const int g = gl / p.n_chunks, hc = gl - g * p.n_chunks;
-  const int G = p.n_rep / p.n_chunks;
-  const int head0 = g * p.n_rep + hc * G;
-  const int ks2 = (int)uni(it.k_s2), vs2 = (int)uni(it.v_s2);
+  const int g = gl / a_n_chunks, hc = gl - g * a_n_chunks;
+  const int G = a_n_rep / a_n_chunks;
+  const int head0 = g * a_n_rep + hc * G;
+  const int gid = ii * a_gpi + gl;
+  unsigned* const gcnt = cset + (size_t)gid * kCtrInts;
+  const bool early = a_early && kpg > 1 && kpg <= kDecodeEarlyMax;
+  // Early protocol: count this part as started; the previous count (and the
+  // merger's give-up mark, if it came first) is read at the end.
+  unsigned started = 0u;
+  if (early && threadIdx.x == 0)
+    started = __hip_atomic_fetch_add(gcnt + kCtrStarted, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // This lane's query elements for the DPP broadcast: qv[h][e][c] =
   // Q[head0 + hb + 4h][64e + 4col + c] (head slots past G repeat head G-1 and
@@ -332,33 +409,23 @@ void decode_kernel(const DecodeParams p) {
   const lds_t* const vbase = ring + C::SUBB + 4 * col * C::ELT;
   lds_t* const pw = lds + C::L_P + wv * (HSL * kDecodeSub * 4);  // this wave's P area
 
-  // Request stream: this workgroup's share [a, b) of the group's positions in
-  // sub-tiles of 16 (the last one partial). The waves take the sub-tiles in
-  // turn from a workgroup counter in LDS as they refill their slots, so a wave
-  // that is served faster takes more and the waves finish together. Rows past
-  // b lie outside the sub-tile's bounded resource and arrive as zeros without
-  // a memory request; a take past the share refills through a zero-sized
-  // resource. rows[s]: first position of the sub-tile in ring slot s, or -1.
-  const int a = (int)((int64_t)n_kv * part / kpg), b = (int)((int64_t)n_kv * (part + 1) / kpg);
-  const unsigned nsub = (unsigned)((b - a + kDecodeSub - 1) / kDecodeSub);
-  const int gid = ii * p.n_head_kv * p.n_chunks + gl;
+  // Request stream over the group's sub-tiles [0, nsub) of 16 positions (the
+  // last one partial: its rows past n_kv lie outside the sub-tile's bounded
+  // resource and arrive as zeros without a memory request). rows[s]: first
+  // position of the sub-tile in ring slot s, or -1 once the wave has run out.
+  const int nsub = (n_kv + kDecodeSub - 1) / kDecodeSub;
   const rsrc_t none = make_rsrc(it_k, 0u);
   const char* const kg = it_k + (int64_t)g * k_s1;
   const char* const vg = it_v + (int64_t)g * v_s1;
-  __attribute__((address_space(3))) unsigned* const take =
-      reinterpret_cast<__attribute__((address_space(3))) unsigned*>(lds + C::L_FLAG + 4);
   int rows[NB];
-  auto refill = [&](auto slc) __attribute__((always_inline)) {
+  auto issue = [&](auto slc, int t) __attribute__((always_inline)) {
     constexpr int SL = decltype(slc)::value;
     lds_t* const slot = ring + SL * C::SLOTB;
-    unsigned t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(take, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
     rsrc_t kr = none, vr = none;
     rows[SL] = -1;
     if (t < nsub) {
-      const int r0 = a + kDecodeSub * (int)t;
-      const int nr = min(kDecodeSub, b - r0);
+      const int r0 = kDecodeSub * t;
+      const int nr = min(kDecodeSub, n_kv - r0);
       kr = make_rsrc(kg + (int64_t)r0 * ks2, (unsigned)((nr - 1) * ks2 + C::RB));
       vr = make_rsrc(vg + (int64_t)r0 * vs2, (unsigned)((nr - 1) * vs2 + C::RB));
       rows[SL] = r0;
@@ -368,7 +435,39 @@ void decode_kernel(const DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < C::NDK; ++i) dma16(vr, slot + C::SUBB + 1024 * i, offv[i]);
   };
-  static_for<0, NB>([&](auto slc) { refill(slc); });
+  // Dynamic takes: pend[s] is the claim (issued by lane 0 one ring cycle ago)
+  // that names slot s's next sub-tile, nst + claim, after the fixed prefix of
+  // nst = NB kpg NWV sub-tiles (wave wv of part `part` starts with sub-tile
+  // (s kpg + part) NWV + wv in slot s). Claims of one slot are sequential, so
+  // once a slot's claim runs past the group every later one does too.
+  const int nst = NB * kpg * NWV;
+  unsigned* const claim_ctr = gcnt + kCtrClaim;
+  unsigned pend[NB];
+  __attribute__((address_space(3))) unsigned* const take =
+      reinterpret_cast<__attribute__((address_space(3))) unsigned*>(lds + C::L_FLAG + 4);
+  // Local takes: the workgroup's t-th sub-tile is part + kpg t.
+  auto lds_take = [&]() __attribute__((always_inline)) {
+    unsigned t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(take, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    t = min((unsigned)__builtin_amdgcn_readfirstlane((int)t), (unsigned)nsub);
+    return (int)min((unsigned)part + (unsigned)kpg * t, (unsigned)nsub);
+  };
+  auto refill = [&](auto slc, bool first) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slc)::value;
+    int t;
+    if constexpr (DYN) {
+      t = first ? (SL * kpg + part) * NWV + wv
+                : (int)min((unsigned)nst + (unsigned)__builtin_amdgcn_readfirstlane((int)pend[SL]),
+                           (unsigned)nsub);
+      unsigned c = 0;
+      if (lane == 0) c = __hip_atomic_fetch_add(claim_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pend[SL] = c;
+    } else {
+      t = lds_take();
+    }
+    issue(slc, t);
+  };
+  static_for<0, NB>([&](auto slc) { refill(slc, true); });
   // The queries were requested first; they are in registers once at most the
   // ring's loads are outstanding (the empty asm makes the compiler wait here).
 #pragma unroll
@@ -431,14 +530,14 @@ void decode_kernel(const DecodeParams p) {
     });
 
     // Online softmax (base 2); the running max is uniform over a row.
-    const bool valid = row0 + col < b;
+    const bool valid = row0 + col < n_kv;
     float pr[HS];
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
       float x = s[h][0];
 #pragma unroll
       for (int t = 1; t < NACC; ++t) x += s[h][t];
-      x = valid ? x * p.scale_log2e : -INFINITY;
+      x = valid ? x * a_scale_log2e : -INFINITY;
       const float mn = fmaxf(m[h], row_max16(x));
       const float alpha = fast_exp2(m[h] - mn);
       pr[h] = fast_exp2(x - mn);
@@ -477,40 +576,26 @@ void decode_kernel(const DecodeParams p) {
       }
     wave_lds_fence();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot reads done before it is refilled
-    refill(slc);
   };
 
-  // Ring slots are used in turn until the first slot without a sub-tile (a
-  // wave's takes increase, so every later slot is empty too).
-  if (rows[0] >= 0) {
-    for (;;) {
-      bool done = false;
-      static_for<0, NB>([&](auto slc) {
-        constexpr int SL = decltype(slc)::value;
-        if (!done) {
-          process(slc);
-          done = rows[(SL + 1) % NB] < 0;
-        }
-      });
-      if (done) break;
-    }
+  // Ring slots in turn; a slot with a sub-tile is processed, every slot is
+  // refilled; the loop ends once no slot holds a sub-tile.
+  for (;;) {
+    static_for<0, NB>([&](auto slc) {
+      constexpr int SL = decltype(slc)::value;
+      if (rows[SL] >= 0) process(slc);
+      refill(slc, false);
+    });
+    bool any = false;
+#pragma unroll
+    for (int s = 0; s < NB; ++s) any |= rows[s] >= 0;
+    if (!any) break;
   }
 
   // The waves meet in LDS: wave w's deposit at the start of its ring, once
-  // its last loads (including the zero-filling ones past the share) landed.
+  // its last loads (including the zero-filling ones) landed.
   wait_vmem<0>();
-  // Early protocol (groups of 2..kDecodeEarlyMax workgroups, every workgroup
-  // of the launch resident): the group's first workgroup to get here merges,
-  // the others only store stamped records. The claim's round trip overlaps
-  // the deposits.
-  unsigned* const gcnt = p.cnt + (int64_t)gid * p.cst;
   unsigned* const flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
-  const bool early = p.early && kpg > 1 && kpg <= kDecodeEarlyMax;
-  // (As asm, so that the compiler's wait before the deposits' LDS writes does
-  // not wait for it: the result is waited for explicitly below.)
-  unsigned claim = 1u;
-  if (early && threadIdx.x == 0)
-    asm volatile("global_atomic_add %0, %1, %2, off sc0" : "=v"(claim) : "v"(gcnt), "v"(1u) : "memory");
   auto dep_at = [&](int w) { return reinterpret_cast<float*>(lds_dyn + C::L_RING + w * NB * C::SLOTB); };
 #pragma unroll
   for (int h = 0; h < HS; ++h) l[h] = row_sum16(l[h]);
@@ -528,42 +613,49 @@ void decode_kernel(const DecodeParams p) {
       }
     }
   }
-  if (early && threadIdx.x == 0) {
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(claim) : : "memory");
-    flag[0] = claim == 0u;
-  }
   wg_barrier();
-  const bool merger = early && __builtin_amdgcn_readfirstlane(flag[0]) != 0;
+  const bool merger = early && part == 0;
   float* const own = reinterpret_cast<float*>(lds_dyn + C::L_OWN);
+  const unsigned long long ep = (unsigned long long)a_epoch << 32;
+  constexpr unsigned long long kHi = 0xffffffff00000000ull;
 
-  // The early merger: every part's partial in part order (its own from LDS,
-  // the others' stamped records polled until their words carry this launch's
-  // epoch; the other parts started before this workgroup finished and all of
-  // the launch's workgroups are resident, so they complete; a bounded poll
-  // count still ends the wait, with NaN output), subsets combined in order,
-  // O written, the claim counter re-armed (every other part claimed before it
-  // stored, so no increment is still in flight).
-  auto merge_early = [&]() __attribute__((always_inline)) {
+  // Stamped record words of part q (early protocol): acc value c of pair
+  // (hs, cq) at word hs (D + 2) + c D/4 + cq (consecutive lanes, whole
+  // sectors), m at hs (D + 2) + D, l at + D + 1. 64-bit agent-scope atomics
+  // keep each word whole: a reader that sees this launch's epoch in a word has
+  // that word's value.
+  auto rec_word = [&](int q, int hs, int k, int cq) __attribute__((always_inline)) {
+    return reinterpret_cast<unsigned long long*>(a_rec) + (int64_t)(wg - part + q) * (C::REC / 2) +
+           hs * (D + 2) + (k < 4 ? k * (D / 4) + cq : D + (k - 4));
+  };
+  auto store_stamped = [&](int hs, int cq, float mx, float lt, f32x4 at) __attribute__((always_inline)) {
+    auto pk = [&](float v) { return ep | __builtin_bit_cast(unsigned, v); };
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      __hip_atomic_store(rec_word(part, hs, c, cq), pk(at[c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (cq == 0) {
+      __hip_atomic_store(rec_word(part, hs, 4, 0), pk(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(rec_word(part, hs, 5, 0), pk(lt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+
+  // Early merge: every part's partial in part order -- part `own_part`'s from
+  // LDS (-1: none), the others' stamped records polled until their words carry
+  // this launch's epoch, at most `polls` rounds. Subsets combined in order. On
+  // success O is written and true returned; otherwise nothing is written.
+  auto merge_early = [&](int own_part, int polls) __attribute__((always_inline)) -> bool {
     constexpr int NP = C::NP, NSUB = C::NSUB;
     constexpr int RB = (kDecodeEarlyMax + NSUB - 1) / NSUB;  // parts per subset
-    constexpr int kMaxPolls = 1 << 22;
     wg_barrier();  // the own partial is in LDS
     const int tt = threadIdx.x;
     const int pair = tt % NP, sub = tt / NP;
     const int hs = pair / (D / 4), cq = pair % (D / 4);
     float mx = -INFINITY, lt = 0.f;
     f32x4 at = {0.f, 0.f, 0.f, 0.f};
-    bool lost = false;
+    bool fresh = true;
     if (sub < NSUB) {
-      // word k of part q's record for this pair: acc values 0-3, then m, l
-      const unsigned long long* const g0 =
-          reinterpret_cast<const unsigned long long*>(p.rec) + (int64_t)(wg - part) * (C::REC / 2) + hs * (D + 2);
-      auto word = [&](int i, int k) __attribute__((always_inline)) {
-        return g0 + (int64_t)min(sub + i * NSUB, kpg - 1) * (C::REC / 2) + (k < 4 ? k * (D / 4) + cq : D + (k - 4));
-      };
-      auto polled = [&](int i) { return sub + i * NSUB < kpg && sub + i * NSUB != part; };
-      const unsigned long long ep = (unsigned long long)p.epoch << 32;
-      constexpr unsigned long long kHi = 0xffffffff00000000ull;
+      auto polled = [&](int i) { return sub + i * NSUB < kpg && sub + i * NSUB != own_part; };
+      auto word = [&](int i, int k) { return rec_word(min(sub + i * NSUB, kpg - 1), hs, k, cq); };
       unsigned long long w[RB][6];
 #pragma unroll
       for (int i = 0; i < RB; ++i)
@@ -571,16 +663,12 @@ void decode_kernel(const DecodeParams p) {
         for (int k = 0; k < 6; ++k)
           w[i][k] = polled(i) ? __hip_atomic_load(word(i, k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : ep;
       for (int n = 0;; ++n) {
-        bool fresh = true;
+        fresh = true;
 #pragma unroll
         for (int i = 0; i < RB; ++i)
 #pragma unroll
           for (int k = 0; k < 6; ++k) fresh &= (w[i][k] & kHi) == ep;
-        if (fresh) break;
-        if (n == kMaxPolls) {
-          lost = true;
-          break;
-        }
+        if (fresh || n >= polls) break;
 #pragma unroll
         for (int i = 0; i < RB; ++i)
 #pragma unroll
@@ -593,7 +681,7 @@ void decode_kernel(const DecodeParams p) {
         const int q = sub + i * NSUB;
         if (q < kpg) {
           float v[6];
-          if (q == part) {
+          if (q == own_part) {
             const float* e = own + pair * 6;
             v[0] = e[2]; v[1] = e[3]; v[2] = e[4]; v[3] = e[5]; v[4] = e[0]; v[5] = e[1];
           } else {
@@ -609,11 +697,17 @@ void decode_kernel(const DecodeParams p) {
         }
       }
     }
+    // every subset's thread agrees on freshness before anything is written
+    flag[2] = 1u;
+    wg_barrier();
+    if (!fresh) flag[2] = 0u;
+    wg_barrier();
+    if (flag[2] == 0u) return false;
     if constexpr (NSUB > 1) {
       float* tmp = reinterpret_cast<float*>(lds_dyn + C::L_TMP);
       if (sub < NSUB) {
         tmp[(sub * NP + pair) * 6 + 0] = mx;
-        tmp[(sub * NP + pair) * 6 + 1] = lost ? NAN : lt;  // a lost record makes the output NaN
+        tmp[(sub * NP + pair) * 6 + 1] = lt;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) tmp[(sub * NP + pair) * 6 + 2 + jj] = at[jj];
       }
@@ -633,10 +727,18 @@ void decode_kernel(const DecodeParams p) {
     }
     if (sub == 0 && hs < G) {
       float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
-      gstore<f32x4>(o + 4 * cq, lost ? f32x4{NAN, NAN, NAN, NAN} : at * (1.f / lt));
+      gstore<f32x4>(o + 4 * cq, at * (1.f / lt));
     }
-    if (tt == 0) __hip_atomic_store(gcnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
   };
+  // Thread 0's returning agent-scope atomic add, its result broadcast.
+  auto atomic_bcast = [&](unsigned* c, unsigned inc) __attribute__((always_inline)) {
+    wg_barrier();
+    if (threadIdx.x == 0) flag[1] = __hip_atomic_fetch_add(c, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wg_barrier();
+    return (unsigned)__builtin_amdgcn_readfirstlane((int)flag[1]);
+  };
+
   {
     // wave wv combines head slots wv + NWV t; lane = (slot t, float4 cq)
     constexpr int SPW = (HSL + NWV - 1) / NWV;  // head slots per wave
@@ -669,22 +771,7 @@ void decode_kernel(const DecodeParams p) {
         *reinterpret_cast<f32x2*>(e + 2) = f32x2{at[0], at[1]};
         *reinterpret_cast<f32x2*>(e + 4) = f32x2{at[2], at[3]};
       } else if (early) {
-        // 64-bit words (value bits, launch epoch), written and read with 64-bit
-        // agent-scope atomics (wider accesses may split): acc value c of pair
-        // (hs, cq) at word hs (D + 2) + c D/4 + cq (consecutive lanes, whole
-        // sectors), m at hs (D + 2) + D, l at + D + 1. A reader that sees this
-        // launch's epoch in a word has that word's value.
-        unsigned long long* const rw = reinterpret_cast<unsigned long long*>(p.rec) +
-                                       (int64_t)wg * (C::REC / 2) + hs * (D + 2);
-        const unsigned long long ep = (unsigned long long)p.epoch << 32;
-        auto pk = [&](float v) { return ep | __builtin_bit_cast(unsigned, v); };
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          __hip_atomic_store(rw + c * (D / 4) + cq, pk(at[c]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (cq == 0) {
-          __hip_atomic_store(rw + D, pk(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(rw + D + 1, pk(lt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        store_stamped(hs, cq, mx, lt, at);
       } else {
         const unsigned r0 = (unsigned)(wg * C::REC * 4);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, at), recr,
@@ -695,24 +782,77 @@ void decode_kernel(const DecodeParams p) {
       }
     }
   }
-  if (kpg == 1 || (early && !merger)) return;
-  if (merger) {
-    merge_early();
+  if (kpg == 1) return;
+  if (early) {
+    constexpr unsigned kGaveUp = 1u << 16;
+    constexpr int kLongWait = 1 << 20;  // rounds; only a broken invariant exhausts it
+    int own_part = part;
+    if (!merger) {
+      // The record is stored. Parts that started before any give-up mark
+      // leave the merge to the merger (it keeps waiting for them); a part
+      // that started after it counts itself among the late parts, and the
+      // last of those merges.
+      if (threadIdx.x == 0) flag[3] = started;
+      wg_barrier();
+      const unsigned st = (unsigned)__builtin_amdgcn_readfirstlane((int)flag[3]);
+      if ((st & kGaveUp) == 0u) return;
+      unsigned at = 0u;  // parts started before the mark, plus one (written by the merger)
+      for (int n = 0; n < kLongWait && at == 0u; ++n)
+        at = __hip_atomic_load(gcnt + kCtrGaveUpAt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int late = kpg - (int)(at - 1u);
+      const unsigned d = atomic_bcast(gcnt + kCtrLate, 1u);
+      if (at == 0u || (int)d != late - 1) return;
+      own_part = -1;  // its own record is stored like the others
+    } else if (!merge_early(part, a_max_polls)) {
+      // Out of polls: mark the start counter. If every part had started, all
+      // are running: keep waiting. Otherwise store this part's partial as a
+      // stamped record, publish the give-up point and leave the merge to the
+      // last late part.
+      const unsigned g0 = atomic_bcast(gcnt + kCtrStarted, kGaveUp);
+      if ((int)(g0 & (kGaveUp - 1)) < kpg) {
+        constexpr int NP = C::NP;
+        for (int pr = threadIdx.x; pr < NP; pr += NWV * kWave) {
+          const float* e = own + pr * 6;
+          store_stamped(pr / (D / 4), pr % (D / 4), e[0], e[1], f32x4{e[2], e[3], e[4], e[5]});
+        }
+        wait_vmem<0>();
+        if (threadIdx.x == 0) {
+          __hip_atomic_store(gcnt + kCtrGaveUpAt, (g0 & (kGaveUp - 1)) + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(a_status + 0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+      }
+    } else {
+      return;
+    }
+    // Every part of the group is running or done: merge all partials (from
+    // LDS for own_part, the rest from their records). The bound only guards
+    // against a broken invariant (then the output is NaN and the group is
+    // counted as lost).
+    if (!merge_early(own_part, kLongWait)) {
+      constexpr int NP = C::NP;
+      for (int pr = threadIdx.x; pr < NP; pr += NWV * kWave) {
+        const int hs = pr / (D / 4), cq = pr % (D / 4);
+        if (hs < G) {
+          float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
+          gstore<f32x4>(o + 4 * cq, f32x4{NAN, NAN, NAN, NAN});
+        }
+      }
+      if (threadIdx.x == 0) __hip_atomic_fetch_add(a_status + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     return;
   }
   wait_vmem<0>();  // the record stores have completed
 
-  // Cross-workgroup combine. The group's workgroups form teams of up to TEAM
-  // (as many records as one merge round below reads). The last workgroup to
-  // arrive in a team merges the team's records; with one team it writes O,
-  // otherwise it stores the result as the record of the team's first part
-  // and the last team to arrive merges the team records and writes O. Each
-  // merger re-arms the counter it completed. Counters of group gid:
-  // cnt[gid * cst] (teams), cnt[gid * cst + 1 + team].
+  // Team protocol. The group's workgroups form teams of up to TEAM (as many
+  // records as one merge round below reads). The last workgroup to arrive in
+  // a team merges the team's records; with one team it writes O, otherwise it
+  // stores the result as the record of the team's first part and the last
+  // team to arrive merges the team records and writes O.
   constexpr int NP = C::NP, NSUB = C::NSUB;
   static_assert(NSUB >= 1, "one pair per thread");
   constexpr int RB8 = 8;                      // records per subset requested at once
-  constexpr int TEAM = NSUB * RB8;            // records one round reads
+  constexpr int TEAM = C::TEAM;               // records one round reads
   const int n_teams = (kpg + TEAM - 1) / TEAM;
   const int team = part / TEAM, team_first = team * TEAM;
   const int team_n = min(TEAM, kpg - team_first);
@@ -726,7 +866,7 @@ void decode_kernel(const DecodeParams p) {
     wg_barrier();
     return __builtin_amdgcn_readfirstlane(flag[0]) != 0;
   };
-  if (!arrive(gcnt + 1 + team, team_n)) return;
+  if (!arrive(gcnt + kCtrTeams + team, team_n)) return;
 
   const int tt = threadIdx.x;
   const int pair = tt % NP, sub = tt / NP;
@@ -798,7 +938,6 @@ void decode_kernel(const DecodeParams p) {
   float mx, lt;
   f32x4 at;
   merge(team_first, team_n, 1, mx, lt, at);
-  if (tt == 0) __hip_atomic_store(gcnt + 1 + team, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (n_teams == 1) {
     write_out(lt, at);
     return;
@@ -812,10 +951,9 @@ void decode_kernel(const DecodeParams p) {
                                             r0 + 4 * (HSL * D + 2 * hs), 0, kSc1);
   }
   wait_vmem<0>();
-  if (!arrive(gcnt, n_teams)) return;
+  if (!arrive(gcnt + kCtrElect, n_teams)) return;
   merge(0, n_teams, TEAM, mx, lt, at);
   write_out(lt, at);
-  if (tt == 0) __hip_atomic_store(gcnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Waves per workgroup: two per SIMD at head_dim 64 (a 128 KB ring still gives
@@ -826,27 +964,36 @@ constexpr int decode_waves() {
   return D == 64 ? 8 : 4;
 }
 
-template <int D, typename KT, int HS>
+template <int D, typename KT, int HS, bool DYN>
 static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
   constexpr int NWV = decode_waves<D, KT>();
-  typedef DecodeCfg<D, KT, HS, NWV> C;
+  typedef DecodeCfg<D, KT, HS, NWV, DYN> C;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, KT, HS, NWV>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, KT, HS, NWV, DYN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, C::L_TOTAL);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV>), dim3((unsigned)p.n_wg), dim3(NWV * kWave),
+  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV, DYN>), dim3((unsigned)p.n_wg), dim3(NWV * kWave),
                      C::L_TOTAL, stream, p);
   return hipGetLastError();
 }
 
 template <int D, typename KT>
-static hipError_t launch_decode_h(const DecodeParams& p, int group, hipStream_t stream) {
-  return group > 4 ? launch_decode_t<D, KT, 2>(p, stream) : launch_decode_t<D, KT, 1>(p, stream);
+static hipError_t launch_decode_h(const DecodeParams& p, int group, bool dyn, hipStream_t stream) {
+  if (group > 4)
+    return dyn ? launch_decode_t<D, KT, 2, true>(p, stream) : launch_decode_t<D, KT, 2, false>(p, stream);
+  return dyn ? launch_decode_t<D, KT, 1, true>(p, stream) : launch_decode_t<D, KT, 1, false>(p, stream);
 }
 
 int decode_wg_waves(int head_dim, bool f16) {
   (void)f16;
   return head_dim == 64 ? 8 : 4;
+}
+
+int decode_ring_slots(int head_dim, bool f16) {
+  const int rb = head_dim * (f16 ? 2 : 4);
+  const int ring = (head_dim == 128 && f16 ? 64 : 128) * 1024;
+  const int nb = ring / (decode_wg_waves(head_dim, f16) * 2 * kDecodeSub * rb);
+  return nb > 4 ? 4 : nb;
 }
 
 // Records one merge round reads (the team size of the cross-workgroup combine).
@@ -868,15 +1015,28 @@ size_t decode_record_floats(int head_dim, int group) {
   return (size_t)(2 * hsl * (head_dim + 2));  // room for the early protocol's 64-bit words
 }
 
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, bool dyn,
                          hipStream_t stream) {
   if (head_dim == 64)
-    return f16 ? launch_decode_h<64, _Float16>(p, group, stream)
-               : launch_decode_h<64, float>(p, group, stream);
+    return f16 ? launch_decode_h<64, _Float16>(p, group, dyn, stream)
+               : launch_decode_h<64, float>(p, group, dyn, stream);
   if (head_dim == 128)
-    return f16 ? launch_decode_h<128, _Float16>(p, group, stream)
-               : launch_decode_h<128, float>(p, group, stream);
+    return f16 ? launch_decode_h<128, _Float16>(p, group, dyn, stream)
+               : launch_decode_h<128, float>(p, group, dyn, stream);
   return hipErrorInvalidValue;
+}
+
+// Sets n words at p to v (workspace resets; a kernel rather than a memset so
+// that it may be recorded in a graph).
+__global__ __launch_bounds__(256) void fill_u32_kernel(unsigned* p, size_t n, unsigned v) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = v;
+}
+
+hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, stream, p, n, v);
+  return hipGetLastError();
 }
 
 }  // namespace mi

@@ -13,12 +13,17 @@ namespace mi {
 // decode.hip
 int decode_group_size(int n_rep);                       // G: Q heads per group
 int decode_wg_waves(int head_dim, bool f16);            // waves per decode workgroup
+int decode_ring_slots(int head_dim, bool f16);          // ring slots per wave
 size_t decode_record_floats(int head_dim, int group);   // floats per cross-workgroup record
 int decode_team(int head_dim, bool f16, int group);     // workgroups per combine team
-// p.rec / p.cnt: one record per workgroup and p.cst arrival counters per group
-// (zero on entry, left zero on exit).
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group,
+// p.rec: one record per workgroup; p.cnt: two counter sets (the set of the
+// launch's epoch parity is zero on entry; the other is cleared). dyn: the
+// waves claim sub-tiles from the group counters (required when any item has
+// kpg > 1); otherwise each workgroup takes its group's sub-tiles from LDS.
+hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, bool dyn,
                          hipStream_t stream);
+// n words at p set to v on `stream` (a kernel, so it may sit in a graph).
+hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t stream);
 
 // prefill.hip
 hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu,

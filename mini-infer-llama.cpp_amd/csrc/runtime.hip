@@ -52,18 +52,31 @@ int hip_fail(hipError_t e, const char* what) {
 // ---------------------------------------------------------------------------
 // Library state and device allocation accounting
 // ---------------------------------------------------------------------------
+// Tuning knobs, read from the environment once, at mi_hip_init:
+//   MI_HIP_DECODE_KPG=n    forces n workgroups per decode group
+//   MI_HIP_DECODE_EARLY=0  disables the early merge protocol
+//   MI_HIP_DECODE_SOLO=n   groups of at most n ring loads' worth of sub-tiles
+//                          get one workgroup (no cross-workgroup merge)
+//   MI_HIP_DECODE_CLAIM=n  claim sub-tiles from device counters when each wave
+//                          streams at least n ring loads (0, the default: never;
+//                          measured slower on MI355X at every shape tried, since a
+//                          claim's round trip holds up the loads issued after it)
+struct Knobs {
+  int kpg = 0;
+  int early = 1;
+  int solo = 1;
+  int claim = 0;
+};
+
 struct State {
   std::mutex mu;
   int device = -1;
   bool ready = false;
   std::atomic<uint64_t> n_malloc{0}, n_free{0}, live{0}, peak{0};
   std::atomic<uint64_t> limit{0};
-  // Decode workspace (arrival counters and cross-workgroup records), grown on
-  // demand, never shrunk.
-  char* ws = nullptr;
-  size_t ws_bytes = 0;
-  uint32_t epoch = 0;  // stamp of the last decode launch
   int n_cu = 0;  // compute units of the device
+  Knobs knobs;
+  mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
 };
 State g;
 
@@ -96,46 +109,6 @@ int bind_device() {
   return MI_HIP_OK;
 }
 
-// Workspace layout: the decode arrival counters (kCounterBytes, zero between
-// launches), then the decode records. Grows to at least `rec_bytes` of records;
-// growth synchronises the device first, so no in-flight kernel still uses the
-// old buffer, and the new counters start at zero.
-constexpr size_t kCounterBytes = 64 * 1024;
-
-int ensure_workspace(size_t rec_bytes) {
-  const size_t need = kCounterBytes + ((rec_bytes + 255) & ~size_t(255));
-  std::lock_guard<std::mutex> lk(g.mu);
-  if (g.ws && g.ws_bytes >= need) return MI_HIP_OK;
-  if (g.ws) {
-    MI_TRY_HIP(hipDeviceSynchronize(), "hipDeviceSynchronize");
-    dev_free(g.ws, g.ws_bytes);
-    g.ws = nullptr;
-    g.ws_bytes = 0;
-  }
-  void* p = nullptr;
-  int rc = dev_alloc(&p, need, "workspace");
-  if (rc) return rc;
-  hipError_t e = hipMemset(p, 0, need);  // counters zero, record stamps 0 (no launch's epoch)
-  if (e == hipSuccess) e = hipDeviceSynchronize();
-  if (e != hipSuccess) {
-    dev_free(p, need);
-    return hip_fail(e, "workspace init");
-  }
-  g.ws = static_cast<char*>(p);
-  g.ws_bytes = need;
-  return MI_HIP_OK;
-}
-
-unsigned* ws_counters() { return reinterpret_cast<unsigned*>(g.ws); }
-
-// The stamp of the next decode launch: never 0, the stamp of zeroed records.
-uint32_t next_epoch() {
-  std::lock_guard<std::mutex> lk(g.mu);
-  if (++g.epoch == 0) g.epoch = 1;
-  return g.epoch;
-}
-float* ws_records() { return reinterpret_cast<float*>(g.ws + kCounterBytes); }
-
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   return v && *v ? std::atoi(v) : dflt;
@@ -149,10 +122,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Decode launch plan. Every group (item, KV head, head chunk) gets kpg
 // workgroups, in proportion to its share of the launch's sub-tiles so that the
 // launch has about one workgroup per CU; at least one, and no more than leave
-// each wave a sub-tile. MI_HIP_DECODE_KPG=n forces kpg (tuning).
+// each wave a sub-tile. A group that one workgroup's ring covers in at most
+// knobs.solo rounds gets one workgroup: its loads are one latency anyway, and
+// it saves the cross-workgroup merge. Sub-tiles are claimed from device
+// counters (balancing a group's workgroups) when some group is split and each
+// of its waves streams at least knobs.claim ring loads, so that a claim's
+// round trip hides behind a ring cycle; otherwise each workgroup owns every
+// kpg-th sub-tile of its group.
 struct DecodePlan {
   int group = 1, n_chunks = 1;
   int n_wg = 0;
+  int uniform_kpg = 0;  // every item's kpg when they agree, else 0
+  bool dyn = false;     // dynamic sub-tile claims
 };
 
 DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim,
@@ -162,33 +143,29 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   p.n_chunks = n_rep / p.group;
   const int gpi = n_head_kv * p.n_chunks;
   const int waves = mi::decode_wg_waves(head_dim, f16);
+  const int ring = waves * mi::decode_ring_slots(head_dim, f16);
   int64_t sub = 0;
   for (int i = 0; i < n_items; ++i) {
     it[i].spg = (it[i].n_kv + mi::kDecodeSub - 1) / mi::kDecodeSub;
     sub += (int64_t)gpi * it[i].spg;
   }
-  const int forced = env_int("MI_HIP_DECODE_KPG", 0);
+  const int forced = g.knobs.kpg;
   int64_t wg = 0;
   for (int i = 0; i < n_items; ++i) {
     const int64_t cap = std::max<int64_t>(1, (it[i].spg + waves - 1) / waves);
     int64_t k = forced > 0 ? forced : (int64_t)g.n_cu * it[i].spg / std::max<int64_t>(1, sub);
+    if (forced <= 0 && it[i].spg <= (int64_t)g.knobs.solo * ring) k = 1;
     k = std::max<int64_t>(1, std::min<int64_t>(k, cap));
     it[i].kpg = (int32_t)k;
     it[i].wg0 = (int32_t)wg;
     wg += (int64_t)gpi * k;
+    if (k > 1 && g.knobs.claim > 0 && it[i].spg >= (int64_t)g.knobs.claim * k * ring) p.dyn = true;
   }
+  p.uniform_kpg = it[0].kpg;
+  for (int i = 1; i < n_items; ++i)
+    if (it[i].kpg != it[0].kpg) p.uniform_kpg = 0;
   p.n_wg = (int)wg;
   return p;
-}
-
-// Record bytes that cover every decode launch of this shape: at most one
-// workgroup per CU plus one per group for the at-least-one rounding.
-size_t decode_rec_bound(int n_head_kv, int n_rep, int head_dim) {
-  const int group = mi::decode_group_size(n_rep);
-  const int64_t groups = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group);
-  const int forced = env_int("MI_HIP_DECODE_KPG", 0);
-  const int64_t wgs = forced > 0 ? groups * forced : g.n_cu + groups;
-  return (size_t)wgs * mi::decode_record_floats(head_dim, group) * sizeof(float);
 }
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
@@ -196,9 +173,117 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 }  // namespace
 
 // ---------------------------------------------------------------------------
+// Decode workspace: [status words][two counter sets][records], each part
+// 256-byte aligned. Zeroed once at creation; afterwards the kernels keep the
+// counter sets zero between launches (see decode.hip) and the epoch stamps
+// make stale records recognisable.
+// ---------------------------------------------------------------------------
+struct mi_hip_workspace {
+  int groups = 0;           // groups one launch may have (counter-set capacity)
+  size_t rec_bytes = 0;     // record capacity
+  char* base = nullptr;
+  size_t bytes = 0;
+  unsigned* status = nullptr;
+  unsigned* cnt = nullptr;
+  float* rec = nullptr;
+  std::mutex mu;
+  uint32_t epoch = 0;       // stamp of the last launch
+  int dirty[2] = {0, 0};    // counter set s: groups [0, dirty[s]) the last launch on it used
+  int32_t max_polls = 4096;
+  bool borrowed = false;    // memory not owned (never freed)
+};
+
+namespace {
+
+constexpr size_t kWsAlign = 256;
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+size_t ws_counter_bytes(int groups) { return 2 * (size_t)groups * mi::kCtrInts * sizeof(unsigned); }
+
+// Bytes of a workspace covering `groups` groups and `rec_bytes` of records.
+size_t ws_total_bytes(int groups, size_t rec_bytes) {
+  return kWsAlign + round_up(ws_counter_bytes(groups), kWsAlign) + round_up(rec_bytes, kWsAlign);
+}
+
+// Lays a workspace over [base, base + bytes).
+void ws_layout(mi_hip_workspace* ws, char* base, int groups, size_t rec_bytes) {
+  ws->base = base;
+  ws->groups = groups;
+  ws->rec_bytes = rec_bytes;
+  ws->bytes = ws_total_bytes(groups, rec_bytes);
+  ws->status = reinterpret_cast<unsigned*>(base);
+  ws->cnt = reinterpret_cast<unsigned*>(base + kWsAlign);
+  ws->rec = reinterpret_cast<float*>(base + kWsAlign + round_up(ws_counter_bytes(groups), kWsAlign));
+}
+
+// Groups and record bytes that cover every decode launch of a head shape: up
+// to kDecodeMaxItems items, at most one workgroup per CU plus one per group
+// (the planner's at-least-one rounding), or the forced kpg.
+void ws_capacity(int n_head_kv, int n_rep, int head_dim, int* groups, size_t* rec_bytes) {
+  const int group = mi::decode_group_size(n_rep);
+  const int64_t gr = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group);
+  const int64_t wgs = g.knobs.kpg > 0 ? gr * g.knobs.kpg : g.n_cu + gr;
+  *groups = (int)gr;
+  *rec_bytes = (size_t)wgs * mi::decode_record_floats(head_dim, group) * sizeof(float);
+}
+
+int ws_create(int groups, size_t rec_bytes, mi_hip_workspace** out) {
+  *out = nullptr;
+  mi_hip_workspace* ws = new (std::nothrow) mi_hip_workspace();
+  if (!ws) return fail(MI_HIP_E_NOMEM, "host allocation failed");
+  void* p = nullptr;
+  const size_t bytes = ws_total_bytes(groups, rec_bytes);
+  int rc = dev_alloc(&p, bytes, "decode workspace");
+  if (rc) {
+    delete ws;
+    return rc;
+  }
+  hipError_t e = hipMemset(p, 0, bytes);  // counters zero, record stamps 0 (no launch's epoch)
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    dev_free(p, bytes);
+    delete ws;
+    return hip_fail(e, "workspace init");
+  }
+  ws_layout(ws, static_cast<char*>(p), groups, rec_bytes);
+  *out = ws;
+  return MI_HIP_OK;
+}
+
+void ws_destroy(mi_hip_workspace* ws) {
+  if (!ws) return;
+  if (!ws->borrowed) dev_free(ws->base, ws->bytes);
+  delete ws;
+}
+
+// The stamp of the next launch on ws, which uses `groups` groups: never 0 (the
+// stamp of zeroed records), and alternating in parity (the counter sets).
+// After 2^32 launches the stamps start again at 2 (even, after the odd
+// 2^32 - 1), and the records are zeroed first so that no stale record can
+// carry a reused stamp. *clear: the groups of the other set that the launch
+// must clear (those the launch before it used).
+int ws_next_epoch(mi_hip_workspace* ws, int groups, hipStream_t stream, uint32_t* epoch, int* clear) {
+  std::lock_guard<std::mutex> lk(ws->mu);
+  if (++ws->epoch == 0) {
+    ws->epoch = 2;
+    hipError_t e = mi::launch_fill_u32(reinterpret_cast<unsigned*>(ws->rec), ws->rec_bytes / 4, 0u, stream);
+    if (e != hipSuccess) return hip_fail(e, "workspace record reset");
+  }
+  const int s = (int)(ws->epoch & 1u);
+  *epoch = ws->epoch;
+  *clear = ws->dirty[s ^ 1];
+  ws->dirty[s ^ 1] = 0;
+  ws->dirty[s] = groups;
+  return MI_HIP_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
 // KV cache object
 // ---------------------------------------------------------------------------
 struct mi_hip_kv {
+  mi_hip_workspace* ws = nullptr;  // its own decode workspace
   mi_hip_kv_desc d;
   char* base = nullptr;
   size_t bytes = 0;
@@ -310,7 +395,16 @@ mi::DecodeItem make_item(const mi_hip_attn_args* a, const Resolved& r) {
   return it;
 }
 
-int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
+// The workspace a decode call uses: the first item's, else its cache's, else
+// the library default.
+mi_hip_workspace* workspace_of(const mi_hip_attn_args* a) {
+  if (a->ws) return a->ws;
+  if (a->kv) return a->kv->ws;
+  return g.default_ws;
+}
+
+int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_workspace* ws) {
+  if (!ws) return fail(MI_HIP_E_STATE, "no decode workspace (the library default is gone)");
   Resolved r0;
   int rc = resolve_kv(&items[0], &r0);
   if (rc) return rc;
@@ -339,30 +433,37 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream) {
     }
     const DecodePlan plan =
         plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16);
-    // arrival counters: one per combine team plus one per group
     const int team = mi::decode_team(r0.head_dim, r0.f16, plan.group);
-    int max_kpg = 1;
-    for (int i = 0; i < cnt; ++i) max_kpg = std::max(max_kpg, (int)p.item[i].kpg);
-    p.cst = 1 + (max_kpg + team - 1) / team;
-    if ((size_t)cnt * gpi * p.cst * sizeof(unsigned) > kCounterBytes)
-      return fail(MI_HIP_E_UNSUPPORTED, "decode launch needs %zu arrival counters (%zu available)",
-                  (size_t)cnt * gpi * p.cst, kCounterBytes / sizeof(unsigned));
+    for (int i = 0; i < cnt; ++i)
+      if ((p.item[i].kpg + team - 1) / team > 64 - mi::kCtrTeams)
+        return fail(MI_HIP_E_UNSUPPORTED, "item %d: %d workgroups per group exceed the merge teams",
+                    base + i, (int)p.item[i].kpg);
     const size_t rec_bytes =
         (size_t)plan.n_wg * mi::decode_record_floats(r0.head_dim, plan.group) * sizeof(float);
-    if ((rc = ensure_workspace(rec_bytes))) return rc;
+    if (cnt * gpi > ws->groups || rec_bytes > ws->rec_bytes)
+      return fail(MI_HIP_E_UNSUPPORTED,
+                  "decode launch of %d groups and %zu record bytes exceeds its workspace (%d groups, "
+                  "%zu bytes): create the workspace for this head shape",
+                  cnt * gpi, rec_bytes, ws->groups, ws->rec_bytes);
     p.n_items = cnt;
     p.n_rep = items[0].n_rep;
     p.n_head_kv = r0.n_head_kv;
     p.n_chunks = plan.n_chunks;
+    p.gpi = gpi;
     p.n_wg = plan.n_wg;
+    p.uniform_kpg = plan.uniform_kpg;
     p.scale_log2e = items[0].scale * kLog2e;
-    p.rec = ws_records();
-    p.cnt = ws_counters();
-    // Early merging needs every workgroup of the launch resident at once (one
-    // per CU, the LDS ring fills a CU): a merger waits for its group's others.
-    p.early = plan.n_wg <= g.n_cu && env_int("MI_HIP_DECODE_EARLY", 1) != 0;
-    p.epoch = next_epoch();
-    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, stream);
+    p.rec = ws->rec;
+    p.cnt = ws->cnt;
+    p.status = ws->status;
+    p.ctr_groups = ws->groups;
+    p.max_polls = ws->max_polls;
+    // The early merge is worth its wait when every workgroup of the launch can
+    // be resident at once (one per CU); it stays correct otherwise.
+    // (knob 2 forces it: tests of the fallback for parts that start late).
+    p.early = g.knobs.early == 2 || (plan.n_wg <= g.n_cu && g.knobs.early != 0);
+    if ((rc = ws_next_epoch(ws, cnt * gpi, stream, &p.epoch, &p.clear_groups))) return rc;
+    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, plan.dyn, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     base += cnt;
   }
@@ -401,11 +502,6 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, g.n_cu, stream);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   return MI_HIP_OK;
-}
-
-// Workspace bytes that cover every decode call on this cache (prefill needs none).
-size_t workspace_for(const mi_hip_kv_desc& d) {
-  return decode_rec_bound(d.n_head_kv, d.n_head / d.n_head_kv, d.head_dim);
 }
 
 // ---------------------------------------------------------------------------
@@ -590,7 +686,20 @@ int mi_hip_init(int device) {
   MI_TRY_HIP(hipSetDevice(device), "hipSetDevice");
   g.device = device;
   g.n_cu = prop.multiProcessorCount;
+  g.knobs.kpg = env_int("MI_HIP_DECODE_KPG", 0);
+  g.knobs.early = env_int("MI_HIP_DECODE_EARLY", 1);
+  g.knobs.solo = env_int("MI_HIP_DECODE_SOLO", 1);
+  g.knobs.claim = env_int("MI_HIP_DECODE_CLAIM", 0);
   g.ready = true;
+  // The default workspace: head_dim up to 128, groups of up to 8 heads, up to
+  // 1024 groups per launch (e.g. 32 items x 32 KV heads), ~11 MB.
+  const int groups = 1024;
+  const size_t rec = (size_t)(g.n_cu + groups) * mi::decode_record_floats(128, 8) * sizeof(float);
+  int rc = ws_create(groups, rec, &g.default_ws);
+  if (rc) {
+    g.ready = false;
+    return rc;
+  }
   t_err[0] = '\0';
   return MI_HIP_OK;
 }
@@ -601,9 +710,8 @@ int mi_hip_shutdown(void) {
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(g.mu);
   (void)hipDeviceSynchronize();
-  dev_free(g.ws, g.ws_bytes);
-  g.ws = nullptr;
-  g.ws_bytes = 0;
+  ws_destroy(g.default_ws);
+  g.default_ws = nullptr;
   g.ready = false;
   g.device = -1;
   return MI_HIP_OK;
@@ -692,7 +800,10 @@ int mi_hip_kv_create(const mi_hip_kv_desc* d, mi_hip_kv** out) {
     delete kv;
     return hip_fail(e, "KV cache init");
   }
-  if ((rc = ensure_workspace(workspace_for(*d)))) {
+  int groups;
+  size_t rec_bytes;
+  ws_capacity(d->n_head_kv, d->n_head / d->n_head_kv, d->head_dim, &groups, &rec_bytes);
+  if ((rc = ws_create(groups, rec_bytes, &kv->ws))) {
     (void)hipStreamDestroy(kv->stream);
     dev_free(kv->stage, kv->stage_bytes);
     dev_free(kv->base, kv->bytes);
@@ -714,9 +825,86 @@ int mi_hip_kv_destroy(mi_hip_kv* kv) {
   }
   (void)hipStreamSynchronize(kv->stream);
   (void)hipStreamDestroy(kv->stream);
+  (void)hipDeviceSynchronize();  // no decode launch on another stream still uses the workspace
+  ws_destroy(kv->ws);
   dev_free(kv->stage, kv->stage_bytes);
   dev_free(kv->base, kv->bytes);
   delete kv;
+  return MI_HIP_OK;
+}
+
+int mi_hip_kv_workspace(mi_hip_kv* kv, mi_hip_workspace** out) {
+  if (!kv || !out) return fail(MI_HIP_E_INVALID, "kv and out must be non-NULL");
+  *out = kv->ws;
+  return MI_HIP_OK;
+}
+
+int mi_hip_workspace_create(const mi_hip_workspace_desc* d, mi_hip_workspace** out) {
+  if (!d || !out) return fail(MI_HIP_E_INVALID, "desc and out must be non-NULL");
+  *out = nullptr;
+  if (d->n_head_kv <= 0 || d->n_head <= 0 || d->n_head % d->n_head_kv != 0)
+    return fail(MI_HIP_E_INVALID, "n_head (%d) must be a positive multiple of n_head_kv (%d)",
+                d->n_head, d->n_head_kv);
+  if (d->head_dim != 64 && d->head_dim != 128)
+    return fail(MI_HIP_E_UNSUPPORTED, "head_dim %d: the kernels cover 64 and 128", d->head_dim);
+  int rc = bind_device();
+  if (rc) return rc;
+  int groups;
+  size_t rec_bytes;
+  ws_capacity(d->n_head_kv, d->n_head / d->n_head_kv, d->head_dim, &groups, &rec_bytes);
+  return ws_create(groups, rec_bytes, out);
+}
+
+int mi_hip_workspace_destroy(mi_hip_workspace* ws) {
+  if (!ws) return MI_HIP_OK;
+  int rc = bind_device();
+  if (rc) return rc;
+  if (ws == g.default_ws) return fail(MI_HIP_E_INVALID, "the default workspace belongs to the library");
+  (void)hipDeviceSynchronize();
+  ws_destroy(ws);
+  return MI_HIP_OK;
+}
+
+int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim) {
+  if (!g.ready) return fail(MI_HIP_E_STATE, "mi_hip_init has not been called");
+  std::lock_guard<std::mutex> lk(g.mu);
+  if (kpg >= 0) g.knobs.kpg = kpg;
+  if (early >= 0) g.knobs.early = early;
+  if (solo >= 0) g.knobs.solo = solo;
+  if (claim >= 0) g.knobs.claim = claim;
+  return MI_HIP_OK;
+}
+
+int mi_hip_workspace_set_poll_limit(mi_hip_workspace* ws, int32_t rounds) {
+  if (!ws || rounds < 0) return fail(MI_HIP_E_INVALID, "ws must be non-NULL and rounds >= 0");
+  std::lock_guard<std::mutex> lk(ws->mu);
+  ws->max_polls = rounds;
+  return MI_HIP_OK;
+}
+
+int mi_hip_workspace_check(mi_hip_workspace* ws, void* stream, mi_hip_workspace_status* out) {
+  if (!ws) return fail(MI_HIP_E_INVALID, "ws is NULL");
+  int rc = bind_device();
+  if (rc) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned words[mi::kStatusWords] = {0, 0, 0, 0};
+  MI_TRY_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  MI_TRY_HIP(hipMemcpyAsync(words, ws->status, sizeof words, hipMemcpyDeviceToHost, st), "status copy");
+  MI_TRY_HIP(hipStreamSynchronize(st), "hipStreamSynchronize");
+  hipError_t e = mi::launch_fill_u32(ws->status, mi::kStatusWords, 0u, st);
+  // A lost record leaves its group's counters wherever they stopped: start over.
+  if (e == hipSuccess && words[1] != 0) {
+    e = mi::launch_fill_u32(ws->cnt, ws_counter_bytes(ws->groups) / sizeof(unsigned), 0u, st);
+    std::lock_guard<std::mutex> lk(ws->mu);
+    ws->dirty[0] = ws->dirty[1] = 0;
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(st);
+  if (e != hipSuccess) return hip_fail(e, "workspace status reset");
+  if (out) {
+    out->early_fallbacks = words[0];
+    out->lost_groups = words[1];
+  }
+  if (words[1] != 0) return fail(MI_HIP_E_LOST, "%u decode group(s) lost a record; outputs of those launches are NaN", words[1]);
   return MI_HIP_OK;
 }
 
@@ -804,7 +992,7 @@ int mi_hip_attn_fwd(const mi_hip_attn_args* a) {
   if ((rc = check_problem(a, r))) return rc;
   if ((rc = bind_device())) return rc;
   hipStream_t st = static_cast<hipStream_t>(a->stream);
-  return a->n_tokens == 1 ? run_decode(a, 1, st) : run_prefill(a, r, st);
+  return a->n_tokens == 1 ? run_decode(a, 1, st, workspace_of(a)) : run_prefill(a, r, st);
 }
 
 int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* stream) {
@@ -822,7 +1010,7 @@ int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* s
       return fail(MI_HIP_E_INVALID, "item %d: shape, type or scale differs from item 0", i);
   }
   if ((rc = bind_device())) return rc;
-  return run_decode(items, n_items, static_cast<hipStream_t>(stream));
+  return run_decode(items, n_items, static_cast<hipStream_t>(stream), workspace_of(&items[0]));
 }
 
 int mi_hip_op_attn_qk(mi_tensor* dst, void* stream) {

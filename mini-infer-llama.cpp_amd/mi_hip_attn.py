@@ -32,7 +32,7 @@ MI_HIP_QWEN2_ATTN_FUSED = 0
 MI_HIP_QWEN2_ATTN_REFERENCE_ORDER = 1
 
 STATUS = {0: "OK", 1: "E_INVALID", 2: "E_NODEVICE", 3: "E_RUNTIME", 4: "E_NOMEM",
-          5: "E_UNSUPPORTED", 6: "E_STATE"}
+          5: "E_UNSUPPORTED", 6: "E_STATE", 7: "E_LOST"}
 
 
 class MiHipError(RuntimeError):
@@ -80,6 +80,15 @@ class KvDesc(ctypes.Structure):
                 ("n_head", ctypes.c_int32), ("type", ctypes.c_int32)]
 
 
+class WorkspaceDesc(ctypes.Structure):
+    _fields_ = [("n_head_kv", ctypes.c_int32), ("n_head", ctypes.c_int32),
+                ("head_dim", ctypes.c_int32)]
+
+
+class WorkspaceStatus(ctypes.Structure):
+    _fields_ = [("early_fallbacks", ctypes.c_uint32), ("lost_groups", ctypes.c_uint32)]
+
+
 class AttnArgs(ctypes.Structure):
     _fields_ = [
         ("kv", ctypes.c_void_p),
@@ -101,6 +110,7 @@ class AttnArgs(ctypes.Structure):
         ("n_tokens", ctypes.c_int32),
         ("scale", ctypes.c_float),
         ("stream", ctypes.c_void_p),
+        ("ws", ctypes.c_void_p),
     ]
 
 
@@ -152,6 +162,12 @@ SIGNATURES = {
     "mi_hip_set_alloc_limit": ([ctypes.c_uint64], _I),
     "mi_hip_kv_create": ([ctypes.POINTER(KvDesc), ctypes.POINTER(ctypes.c_void_p)], _I),
     "mi_hip_kv_destroy": ([_P], _I),
+    "mi_hip_kv_workspace": ([_P, ctypes.POINTER(ctypes.c_void_p)], _I),
+    "mi_hip_workspace_create": ([ctypes.POINTER(WorkspaceDesc), ctypes.POINTER(ctypes.c_void_p)], _I),
+    "mi_hip_workspace_destroy": ([_P], _I),
+    "mi_hip_workspace_check": ([_P, _P, ctypes.POINTER(WorkspaceStatus)], _I),
+    "mi_hip_workspace_set_poll_limit": ([_P, ctypes.c_int32], _I),
+    "mi_hip_decode_tuning": ([ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32], _I),
     "mi_hip_kv_view": ([_P, _I, _I, ctypes.POINTER(ctypes.c_void_p),
                         ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_size_t)], _I),
     "mi_hip_kv_write": ([_P, _I, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_size_t), _I, _P], _I),
@@ -226,6 +242,23 @@ class Lib:
         self.check(self.so.mi_hip_kv_create(ctypes.byref(d), ctypes.byref(h)))
         return h.value
 
+    def workspace_create(self, n_head_kv, n_head, head_dim):
+        d = WorkspaceDesc(n_head_kv, n_head, head_dim)
+        h = ctypes.c_void_p()
+        self.check(self.so.mi_hip_workspace_create(ctypes.byref(d), ctypes.byref(h)))
+        return h.value
+
+    def kv_workspace(self, kv):
+        h = ctypes.c_void_p()
+        self.check(self.so.mi_hip_kv_workspace(kv, ctypes.byref(h)))
+        return h.value
+
+    def workspace_check(self, ws, stream):
+        """(status code, early_fallbacks, lost_groups) since the last check."""
+        st = WorkspaceStatus()
+        rc = self.so.mi_hip_workspace_check(ws, stream, ctypes.byref(st))
+        return rc, st.early_fallbacks, st.lost_groups
+
     def kv_view(self, kv, layer, which):
         data = ctypes.c_void_p()
         ne = (ctypes.c_int64 * 4)()
@@ -251,10 +284,12 @@ def nb3_of(t):
     return (s[2] * es, s[1] * es, s[0] * es)
 
 
-def attn_args(q, out, n_rep, n_past, scale, stream, kv=None, layer=0, k=None, v=None):
+def attn_args(q, out, n_rep, n_past, scale, stream, kv=None, layer=0, k=None, v=None, ws=None):
     """Builds AttnArgs from torch tensors q/out shaped (n_tokens, n_head, head_dim) and
-    either a cache handle + layer or explicit k/v shaped (n_ctx, n_head_kv, head_dim)."""
+    either a cache handle + layer or explicit k/v shaped (n_ctx, n_head_kv, head_dim);
+    ws: an optional decode workspace handle (else the cache's, else the library default)."""
     a = AttnArgs()
+    a.ws = ws
     if kv is not None:
         a.kv = kv
         a.layer = layer

@@ -87,6 +87,49 @@ def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d):
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F32)
 
 
+# Every F16-cache kernel variant: head_dim 64 (8 waves, 4-slot ring) with
+# groups over and under 4 heads, head_dim 128 with groups of at most 4 (one
+# head slot per row, 64 KB ring) and over 4; the Qwen2.5-0.5B shape at short,
+# odd and long contexts.
+@pytest.mark.parametrize("n_rep,hkv,d,n_kv", [(1, 4, 64, 777), (2, 2, 128, 777), (4, 2, 128, 777),
+                                              (7, 2, 64, 1), (7, 2, 64, 17), (7, 2, 64, 777),
+                                              (7, 2, 64, 4096), (8, 1, 128, 2000)])
+def test_decode_f16_cache_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv):
+    print("f16 decode", n_rep, hkv, d, n_kv, flush=True)
+    q, k, v = cpu_attention.make_inputs(900 + 7 * n_rep + d + n_kv, d, n_rep * hkv, hkv, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=True), TOL_F32, "widened")
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
+
+
+@pytest.fixture()
+def tuning(hip):
+    """Sets decode planner knobs for one test and restores the defaults."""
+    def set_(kpg=-1, early=-1, solo=-1, claim=-1):
+        hip.check(hip.mi_hip_decode_tuning(kpg, early, solo, claim))
+    yield set_
+    hip.check(hip.mi_hip_decode_tuning(0, 1, 1, 0))
+
+
+# Forced workgroups per group: the early protocol (2..8 parts, with and without
+# a part that gets no sub-tile), one team (9..32 parts) and several teams
+# (more than 32 parts at head_dim 64, more than 8 at head_dim 128).
+@pytest.mark.parametrize("kpg,early", [(2, 1), (5, 1), (8, 1), (8, 0), (9, 1), (24, 0), (40, 1), (100, 0)])
+@pytest.mark.parametrize("d,f16", [(64, False), (128, True)])
+@pytest.mark.parametrize("claim", [1, 0])
+def test_decode_forced_split(hip, stream, oracle, tuning, kpg, early, d, f16, claim):
+    # claim 1: sub-tiles claimed from the group counter; 0: every kpg-th sub-tile per part
+    print("forced split", kpg, early, d, f16, claim, flush=True)
+    tuning(kpg=kpg, early=early, claim=claim)
+    n_kv = 3000 + 20 * kpg  # long enough that the forced split is not capped below 33 parts
+    hkv = 2 if d == 64 else 4
+    q, k, v = cpu_attention.make_inputs(4100 + kpg + d, d, 7 * hkv, hkv, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=f16)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=f16), TOL_F32)
+
+
 def test_decode_back_to_back_launches_share_no_records(hip, stream, oracle):
     # Two launches of one shape on one stream, no synchronisation between them:
     # they use the same cross-workgroup record slots, and the second must merge
@@ -116,12 +159,121 @@ def test_decode_qwen7b_shape_f16_cache(hip, stream, oracle):
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
 
 
-@pytest.mark.parametrize("early", ["1", "0"])
-def test_decode_batch_24_layers(hip, stream, oracle, monkeypatch, early):
+def batch_24(hip, stream, n_kv, seed0, ws=None, st=None):
+    """24 independent single-layer decode problems at the Qwen2.5-0.5B shape in one
+    mi_hip_attn_decode_batch call; returns (inputs, device outputs)."""
+    import torch
+    n_layers = 24
+    ins, outs, items = [], [], []
+    for layer in range(n_layers):
+        q, k, v = cpu_attention.make_inputs(seed0 + layer, 64, 14, 2, n_kv, 1)
+        ins.append((q, k, v))
+    dev_in = [(dev(q), dev(k), dev(v)) for q, k, v in ins]
+    for layer in range(n_layers):
+        out = torch.full((1, 14, 64), float("nan"), device="cuda")
+        outs.append(out)
+        dq, dk, dv = dev_in[layer]
+        items.append(mh.attn_args(dq, out, 7, n_kv - 1 - layer, 0.125, st or stream, k=dk, v=dv, ws=ws))
+    arr = (mh.AttnArgs * n_layers)(*items)
+    hip.check(hip.mi_hip_attn_decode_batch(arr, n_layers, st or stream))
+    return ins, outs, dev_in
+
+
+def check_batch_24(oracle, ins, outs, n_kv, what=""):
+    for layer, (q, k, v) in enumerate(ins):
+        want = ref_out(oracle, q, k, v, n_kv - 1 - layer, 0.125)
+        assert_close(outs[layer].cpu().numpy(), want, TOL_F32, f"{what} layer {layer}")
+
+
+def test_early_merge_fallback_is_exact(hip, stream, oracle, tuning):
+    # A poll limit of 0 makes every early merger stop polling at once. A merger
+    # whose parts have all started keeps waiting for them; one whose group
+    # straddles the set of resident workgroups (32 items x 2 groups x 8 parts =
+    # 512 workgroups, about two per CU, with the early protocol forced) gives
+    # up, and the last of its parts that started after that merges. Results
+    # must be exact either way, and no group may be lost.
+    import torch
+    ws = hip.workspace_create(2, 14, 64)
+    try:
+        hip.check(hip.mi_hip_workspace_set_poll_limit(ws, 0))
+        for rep in range(3):
+            ins, outs, _ = batch_24(hip, stream, 4096, 7000 + 100 * rep, ws=ws)
+            torch.cuda.synchronize()
+            check_batch_24(oracle, ins, outs, 4096, f"rep {rep}")
+            rc, fallbacks, lost = hip.workspace_check(ws, stream)
+            print("all resident: fallbacks", fallbacks, "lost", lost, flush=True)
+            assert rc == 0 and lost == 0
+        tuning(kpg=8, early=2)
+        hip.check(hip.mi_hip_workspace_destroy(ws))
+        ws = hip.workspace_create(2, 14, 64)  # sized for the forced split
+        hip.check(hip.mi_hip_workspace_set_poll_limit(ws, 0))
+        total = 0
+        for rep in range(4):
+            n, n_kv = 32, 2048
+            qs, ks, vs, outs, items, keep = [], [], [], [], [], []
+            for i in range(n):
+                q, k, v = cpu_attention.make_inputs(7300 + 50 * rep + i, 64, 14, 2, n_kv, 1)
+                qs.append(q); ks.append(k); vs.append(v)
+                dq, dk, dv = dev(q), dev(k), dev(v)
+                out = torch.full((1, 14, 64), float("nan"), device="cuda")
+                keep.append((dq, dk, dv)); outs.append(out)
+                items.append(mh.attn_args(dq, out, 7, n_kv - 1, 0.125, stream, k=dk, v=dv, ws=ws))
+            arr = (mh.AttnArgs * n)(*items)
+            hip.check(hip.mi_hip_attn_decode_batch(arr, n, stream))
+            torch.cuda.synchronize()
+            for i in range(n):
+                assert_close(outs[i].cpu().numpy(), ref_out(oracle, qs[i], ks[i], vs[i], n_kv - 1, 0.125),
+                             TOL_F32, f"rep {rep} item {i}")
+            rc, fallbacks, lost = hip.workspace_check(ws, stream)
+            print("512 workgroups: fallbacks", fallbacks, "lost", lost, flush=True)
+            assert rc == 0 and lost == 0
+            total += fallbacks
+        print("fallbacks over 4 launches", total, flush=True)
+        tuning(kpg=0, early=1)
+        hip.check(hip.mi_hip_workspace_destroy(ws))
+        ws = hip.workspace_create(2, 14, 64)
+        ins, outs, _ = batch_24(hip, stream, 4096, 7500, ws=ws)
+        torch.cuda.synchronize()
+        check_batch_24(oracle, ins, outs, 4096, "default limit")
+        rc, fallbacks, lost = hip.workspace_check(ws, stream)
+        assert rc == 0 and lost == 0
+    finally:
+        hip.check(hip.mi_hip_workspace_destroy(ws))
+
+
+def test_two_workspaces_decode_concurrently(hip, oracle):
+    # Two sequences' decodes on two streams with their own workspaces, issued
+    # without synchronisation so that the launches overlap on the device (each
+    # wants a workgroup on nearly every CU, so neither is wholly resident: the
+    # early mergers' bounded waits and the fallback get exercised too).
+    import torch
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    w1, w2 = hip.workspace_create(2, 14, 64), hip.workspace_create(2, 14, 64)
+    try:
+        runs = []
+        for rep in range(4):
+            for st, ws, seed in ((s1, w1, 8000), (s2, w2, 9000)):
+                ins, outs, keep = batch_24(hip, None, 4096, seed + 100 * rep, ws=ws, st=st.cuda_stream)
+                runs.append((ins, outs, keep))
+        torch.cuda.synchronize()
+        for i, (ins, outs, _) in enumerate(runs):
+            check_batch_24(oracle, ins, outs, 4096, f"launch {i}")
+        for st, ws in ((s1, w1), (s2, w2)):
+            rc, fallbacks, lost = hip.workspace_check(ws, st.cuda_stream)
+            print("fallbacks", fallbacks, flush=True)
+            assert rc == 0 and lost == 0
+    finally:
+        torch.cuda.synchronize()
+        hip.check(hip.mi_hip_workspace_destroy(w1))
+        hip.check(hip.mi_hip_workspace_destroy(w2))
+
+
+@pytest.mark.parametrize("early", [1, 0])
+def test_decode_batch_24_layers(hip, stream, oracle, tuning, early):
     # both cross-workgroup combines at the headline shape (5 workgroups per
     # group): the first finisher polling stamped records, and the counters
     import torch
-    monkeypatch.setenv("MI_HIP_DECODE_EARLY", early)
+    tuning(early=early)
     n_layers, n_kv = 24, 4096
     qs, ks, vs, outs, items = [], [], [], [], []
     for layer in range(n_layers):
