@@ -225,6 +225,18 @@ int mi_hip_attn_fwd(const mi_hip_attn_args* args);
  * No counterpart in the reference (it runs one node per layer). */
 int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* stream);
 
+/* mi_hip_attn_decode_batch for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. It ignores the items' ws and
+ * their caches' workspaces and uses a fixed 4 MB scratch array that each GPU
+ * holds from library load until the process ends (at most 128 groups, i.e.
+ * items x n_head_kv x head chunks, and records for ~460-900 workgroups); a
+ * larger launch fails with MI_HIP_E_UNSUPPORTED. It calls no hipMalloc or
+ * hipFree. Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on the device (different streams, unsynchronised) race and must
+ * not be issued; calls ordered on one stream are safe. */
+int mi_hip_attn_decode_batch_noalloc(const mi_hip_attn_args* items, int n_items, void* stream);
+
 /* ---- node-level operators on device tensors ----------------------------- */
 /*
  * Same signature idea as the engine's kernels (src/ops_cpu.h:3-12): the node

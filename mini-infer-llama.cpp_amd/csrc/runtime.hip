@@ -77,6 +77,7 @@ struct State {
   int n_cu = 0;  // compute units of the device
   Knobs knobs;
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
+  mi_hip_workspace* scratch_ws = nullptr;  // over the static scratch array (never freed)
 };
 State g;
 
@@ -193,6 +194,14 @@ struct mi_hip_workspace {
   bool borrowed = false;    // memory not owned (never freed)
 };
 
+// Scratch of mi_hip_attn_decode_batch_noalloc: a decode workspace laid over a
+// fixed device array (no allocation ever), one per GPU that loads this code
+// object. Its name is only a host-side stand-in; the device address comes
+// from hipGetSymbolAddress at mi_hip_init.
+constexpr size_t kScratchBytes = 4u << 20;
+constexpr int kScratchGroups = 128;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
 
 constexpr size_t kWsAlign = 256;
@@ -246,6 +255,18 @@ int ws_create(int groups, size_t rec_bytes, mi_hip_workspace** out) {
     return hip_fail(e, "workspace init");
   }
   ws_layout(ws, static_cast<char*>(p), groups, rec_bytes);
+  *out = ws;
+  return MI_HIP_OK;
+}
+
+// The workspace over the static scratch array at device address `ptr`.
+int ws_over_scratch(void* ptr, mi_hip_workspace** out) {
+  *out = nullptr;
+  mi_hip_workspace* ws = new (std::nothrow) mi_hip_workspace();
+  if (!ws) return fail(MI_HIP_E_NOMEM, "host allocation failed");
+  const size_t rec = kScratchBytes - (ws_total_bytes(kScratchGroups, 0) - 0);
+  ws_layout(ws, static_cast<char*>(ptr), kScratchGroups, rec & ~(kWsAlign - 1));
+  ws->borrowed = true;
   *out = ws;
   return MI_HIP_OK;
 }
@@ -700,6 +721,22 @@ int mi_hip_init(int device) {
     g.ready = false;
     return rc;
   }
+  // The no-allocation entry point's scratch: this device's copy of the static
+  // array (zero at load, as its counters and record stamps must start).
+  void* sp = nullptr;
+  hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+  if (se != hipSuccess || !sp) {
+    ws_destroy(g.default_ws);
+    g.default_ws = nullptr;
+    g.ready = false;
+    return hip_fail(se != hipSuccess ? se : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+  }
+  if ((rc = ws_over_scratch(sp, &g.scratch_ws))) {
+    ws_destroy(g.default_ws);
+    g.default_ws = nullptr;
+    g.ready = false;
+    return rc;
+  }
   t_err[0] = '\0';
   return MI_HIP_OK;
 }
@@ -712,6 +749,8 @@ int mi_hip_shutdown(void) {
   (void)hipDeviceSynchronize();
   ws_destroy(g.default_ws);
   g.default_ws = nullptr;
+  ws_destroy(g.scratch_ws);  // the array itself stays until the process ends
+  g.scratch_ws = nullptr;
   g.ready = false;
   g.device = -1;
   return MI_HIP_OK;
@@ -1011,6 +1050,25 @@ int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* s
   }
   if ((rc = bind_device())) return rc;
   return run_decode(items, n_items, static_cast<hipStream_t>(stream), workspace_of(&items[0]));
+}
+
+int mi_hip_attn_decode_batch_noalloc(const mi_hip_attn_args* items, int n_items, void* stream) {
+  if (!items || n_items <= 0) return fail(MI_HIP_E_INVALID, "need at least one item");
+  Resolved r0;
+  int rc = resolve_kv(&items[0], &r0);
+  if (rc) return rc;
+  for (int i = 0; i < n_items; ++i) {
+    Resolved r;
+    if ((rc = resolve_kv(&items[i], &r))) return rc;
+    if ((rc = check_problem(&items[i], r))) return rc;
+    if (items[i].n_tokens != 1) return fail(MI_HIP_E_INVALID, "item %d: n_tokens must be 1", i);
+    if (r.head_dim != r0.head_dim || r.f16 != r0.f16 || r.n_head_kv != r0.n_head_kv ||
+        items[i].n_rep != items[0].n_rep || items[i].scale != items[0].scale)
+      return fail(MI_HIP_E_INVALID, "item %d: shape, type or scale differs from item 0", i);
+  }
+  if ((rc = bind_device())) return rc;
+  // run_decode refuses launches beyond the scratch's groups or record bytes.
+  return run_decode(items, n_items, static_cast<hipStream_t>(stream), g.scratch_ws);
 }
 
 int mi_hip_op_attn_qk(mi_tensor* dst, void* stream) {
