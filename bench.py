@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--deterministic", action="store_true",
+                    help="fixed per-wave takes in the fused kernels (mi_hip_set_deterministic)")
     ap.add_argument("--only", default="",
                     help="comma list: decode,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
                          "counter calibration workload, only when named)")
@@ -377,6 +379,8 @@ def main():
     import mi_hip_attn as mh
     lib = mh.lib()
     lib.init(0)
+    if args.deterministic:
+        lib.check(lib.mi_hip_set_deterministic(1))
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream().cuda_stream
     only = set(filter(None, args.only.split(",")))

@@ -132,6 +132,18 @@ int mi_hip_workspace_set_poll_limit(mi_hip_workspace* ws, int32_t rounds);
  * reference. */
 int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim);
 
+/* Deterministic fused attention (on = 1, the default): every wave of the
+ * decode and prefill kernels takes a fixed share of its workgroup's work, so
+ * each output is the same bits on every run with the same inputs and launch
+ * shape (the merges across waves and workgroups run in a fixed order). Off
+ * (0): each wave takes the next piece of work from a counter, so a wave that
+ * memory serves sooner takes more -- about 1% faster on the 24-layer
+ * n_kv 4096 decode, with results that differ from run to run in the last
+ * bits. Process-wide; takes effect for launches issued afterwards. No
+ * counterpart in the reference (its CPU kernels are deterministic by
+ * construction: src/ops_cpu.cpp:38-53). */
+int mi_hip_set_deterministic(int32_t on);
+
 /* ---- device-resident KV cache ------------------------------------------ */
 
 typedef struct mi_hip_kv mi_hip_kv;

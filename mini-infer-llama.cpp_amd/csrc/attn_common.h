@@ -57,14 +57,13 @@ constexpr int kStatusWords = 4;
 // record each when kpg > 1.
 struct DecodeParams {
   // Scalars first: the kernel reads them in one round of scalar loads.
-  int32_t n_items;
   int32_t n_rep;        // Q heads per KV head
   int32_t n_head_kv;
   int32_t n_chunks;     // head chunks per KV head (n_rep / G)
   int32_t gpi;          // groups per item, n_head_kv * n_chunks
-  int32_t n_wg;         // workgroups
-  int32_t uniform_kpg;  // > 0: every item has this kpg, so item = wg / (gpi * kpg)
+  int32_t n_wg;         // workgroups with work (records)
   int32_t early;        // groups of 2..kDecodeEarlyMax workgroups merged by their first finisher
+  int32_t det;          // 1: each wave takes fixed sub-tiles (the same bits on every run)
   int32_t max_polls;    // the early merger's bounded wait (rounds of polls) before it falls back
   int32_t ctr_groups;   // groups one counter set covers
   int32_t clear_groups; // groups [0, clear_groups) of the other counter set to clear
@@ -74,7 +73,7 @@ struct DecodeParams {
   unsigned* cnt;        // two counter sets of ctr_groups * kCtrInts words: launch e uses set
                         // e & 1 (zero on entry) and clears set (e + 1) & 1 for the next launch
   unsigned* status;     // kStatusWords status words
-  DecodeItem item[kDecodeMaxItems];
+  DecodeItem item[kDecodeMaxItems];  // grid row y serves item y
 };
 
 // ---------------------------------------------------------------------------
@@ -95,6 +94,7 @@ struct PrefillParams {
   int32_t n_head, n_rep, n_past, n_tokens;
   int32_t n_qblocks;     // ceil(n_tokens / 32)
   int32_t lone;          // 1: the last query block has a workgroup of its own
+  int32_t det;           // 1: each wave takes fixed units (the same bits on every run)
   float scale_log2e;
 };
 

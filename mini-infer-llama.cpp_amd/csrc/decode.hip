@@ -99,27 +99,6 @@ __device__ inline float row_sum16(float x) {
   return x;
 }
 
-typedef __attribute__((address_space(3))) const DecodeItem lds_item_t;
-
-// Wave-uniform copies of values read from LDS (the compiler cannot prove a
-// load from a uniform LDS address uniform; buffer resources must be scalar).
-__device__ inline int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
-__device__ inline int64_t uni(int64_t x) {
-  const uint64_t u = (uint64_t)x;
-  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(u >> 32)) << 32) |
-                   (uint32_t)__builtin_amdgcn_readfirstlane((int)u));
-}
-template <typename T>
-__device__ inline T* uni(T* x) {
-  return reinterpret_cast<T*>(uni((int64_t)reinterpret_cast<uintptr_t>(x)));
-}
-
-// The launch's item table, staged in LDS at kernel start: kernel arguments are
-// read once, in one parallel round trip, instead of by dependent scalar loads.
-__device__ inline lds_item_t& item_at(const lds_t* tab, int i) {
-  return reinterpret_cast<lds_item_t*>(tab)[i];
-}
-
 // ---------------------------------------------------------------------------
 // DPP multiply-add blocks. v_fmac_f32_dpp with row_newbcast:J takes its first
 // factor from lane J of each row of 16. The compiler does not form it (the
@@ -233,9 +212,7 @@ struct DecodeCfg {
   static constexpr int L_RING = 0;
   static constexpr int L_P = L_RING + NWV * NB * SLOTB;  // per wave: P[head slot][16]
   static constexpr int L_FLAG = L_P + NWV * HSL * kDecodeSub * 4;
-  static constexpr int L_ITEMS = L_FLAG + 16;
-  static constexpr int L_TOTAL = L_ITEMS + kDecodeMaxItems * (int)sizeof(DecodeItem);
-  static_assert(sizeof(DecodeItem) % 16 == 0, "item table copied in 16-byte pieces");
+  static constexpr int L_TOTAL = L_FLAG + 16;
   static_assert(NB >= 2, "ring depth");
   static_assert(SUBB % 1024 == 0, "1 KB load granularity");
   static_assert(L_TOTAL <= 160 * 1024, "LDS budget");
@@ -262,20 +239,31 @@ struct DecodeCfg {
 template <int D, typename KT, int HS, int NWV, bool DYN>
 __global__ __launch_bounds__(NWV* kWave) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
 void decode_kernel(const DecodeParams p) {
-  // Every scalar parameter in one round of scalar loads (the empty asm needs
-  // them all in registers at once; the compiler would otherwise load each
-  // near its first use, in dependent rounds).
-  const int a_n_items = p.n_items, a_n_rep = p.n_rep, a_n_head_kv = p.n_head_kv, a_n_chunks = p.n_chunks;
-  const int a_gpi = p.gpi, a_n_wg = p.n_wg, a_uniform_kpg = p.uniform_kpg, a_early = p.early;
+  // Every scalar parameter and this grid row's item in one round of scalar
+  // loads (the empty asm needs them all in registers at once; the compiler
+  // would otherwise load each near its first use, in dependent rounds). Row y
+  // of the grid serves item y, so the item's address needs no loaded value.
+  const int ii = blockIdx.y;
+  const DecodeItem& it = p.item[ii];
+  const int a_n_rep = p.n_rep, a_n_head_kv = p.n_head_kv, a_n_chunks = p.n_chunks;
+  const int a_gpi = p.gpi, a_n_wg = p.n_wg, a_early = p.early, a_det = p.det;
   const int a_max_polls = p.max_polls, a_ctr_groups = p.ctr_groups, a_clear_groups = p.clear_groups;
   const unsigned a_epoch = p.epoch;
   const float a_scale_log2e = p.scale_log2e;
   float* const a_rec = p.rec;
   unsigned* const a_cnt = p.cnt;
   unsigned* const a_status = p.status;
-  asm volatile("" ::"s"(a_n_items), "s"(a_n_rep), "s"(a_n_head_kv), "s"(a_n_chunks), "s"(a_gpi), "s"(a_n_wg),
-               "s"(a_uniform_kpg), "s"(a_early), "s"(a_max_polls), "s"(a_ctr_groups), "s"(a_clear_groups),
-               "s"(a_epoch), "s"(a_scale_log2e), "s"(a_rec), "s"(a_cnt), "s"(a_status));
+  const char* const it_k = it.k;
+  const char* const it_v = it.v;
+  const float* const it_q = it.q;
+  float* const it_out = it.out;
+  const int64_t k_s1 = it.k_s1, v_s1 = it.v_s1, q_s1 = it.q_s1, o_s1 = it.o_s1;
+  const int n_kv = it.n_kv, kpg = it.kpg, wg0 = it.wg0;
+  const int ks2 = (int)it.k_s2, vs2 = (int)it.v_s2;
+  asm volatile("" ::"s"(a_n_rep), "s"(a_n_head_kv), "s"(a_n_chunks), "s"(a_gpi), "s"(a_n_wg), "s"(a_early), "s"(a_det),
+               "s"(a_max_polls), "s"(a_ctr_groups), "s"(a_clear_groups), "s"(a_epoch), "s"(a_scale_log2e),
+               "s"(a_rec), "s"(a_cnt), "s"(a_status), "s"(it_k), "s"(it_v), "s"(it_q), "s"(it_out), "s"(k_s1),
+               "s"(v_s1), "s"(q_s1), "s"(o_s1), "s"(n_kv), "s"(kpg), "s"(wg0), "s"(ks2), "s"(vs2));
   typedef DecodeCfg<D, KT, HS, NWV, DYN> C;
   constexpr int HSL = C::HSL, NB = C::NB, NSLOT = C::NSLOT, NE = C::NE;
   constexpr int NACC = 4 / HS;
@@ -287,7 +275,6 @@ void decode_kernel(const DecodeParams p) {
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int col = lane & 15;  // QK: position in the sub-tile; PV: column block
   const int hb = lane >> 4;   // head slots hb + 4 h
-  const int wg = blockIdx.x;
 
   // Records: one per workgroup, written and read with agent-coherent (sc1)
   // accesses through this resource (team protocol) or 64-bit atomics (early).
@@ -295,68 +282,24 @@ void decode_kernel(const DecodeParams p) {
 
   // This launch's counter set; the groups the previous launch used in the
   // other set are cleared for the next launch (write-through stores: the next
-  // launch's atomics are performed in memory).
+  // launch's atomics are performed in memory), by every workgroup of the
+  // grid, those past their row's item included.
   const size_t set_words = (size_t)a_ctr_groups * kCtrInts;
   unsigned* const cset = a_cnt + (size_t)(a_epoch & 1u) * set_words;
   {
     unsigned* const other = a_cnt + (size_t)((a_epoch + 1u) & 1u) * set_words;
-    for (int b = wg; b < a_clear_groups; b += a_n_wg)
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x, n_lin = gridDim.x * gridDim.y;
+    for (int b = lin; b < a_clear_groups; b += n_lin)
       if (threadIdx.x < kCtrInts)
         __hip_atomic_store(other + (size_t)b * kCtrInts + threadIdx.x, 0u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   }
-
-  // This workgroup's item. Uniform launches compute it and read its fields
-  // from the kernel arguments with scalar loads; others stage the item table
-  // in LDS (one parallel round trip) and find the item with one ballot.
-  const lds_t* const tab = lds + C::L_ITEMS;
-  if (!DYN && threadIdx.x == 0) lds_store<unsigned>(lds + C::L_FLAG + 4, 0u);  // LDS take counter
-  int ii;
-  const char* it_k;
-  const char* it_v;
-  const float* it_q;
-  float* it_out;
-  int64_t k_s1, v_s1, q_s1, o_s1;
-  int n_kv, kpg, wg0, ks2, vs2;
-  if (a_uniform_kpg > 0) {
-    if (!DYN) wg_barrier();
-    ii = wg / (a_gpi * a_uniform_kpg);
-    const DecodeItem& it = p.item[ii];
-    it_k = it.k;
-    it_v = it.v;
-    it_q = it.q;
-    it_out = it.out;
-    k_s1 = it.k_s1;
-    v_s1 = it.v_s1;
-    q_s1 = it.q_s1;
-    o_s1 = it.o_s1;
-    n_kv = it.n_kv;
-    kpg = it.kpg;
-    wg0 = it.wg0;
-    ks2 = (int)it.k_s2;
-    vs2 = (int)it.v_s2;
-  } else {
-    constexpr int V16 = kDecodeMaxItems * (int)(sizeof(DecodeItem) / 16);
-    for (int i = threadIdx.x; i < V16; i += NWV * kWave)
-      lds_store<f32x4>(lds + C::L_ITEMS + 16 * i, reinterpret_cast<const f32x4*>(&p.item[0])[i]);
+  // Rows are as wide as the launch's widest item.
+  if ((int)blockIdx.x >= a_gpi * kpg) return;
+  const int wg = wg0 + (int)blockIdx.x;  // this workgroup's record
+  if (!DYN) {
+    if (threadIdx.x == 0) lds_store<unsigned>(lds + C::L_FLAG + 4, 0u);  // LDS take counter
     wg_barrier();
-    // the number of items after the first whose first workgroup is at or below this one
-    const int w0 = item_at(tab, lane & (kDecodeMaxItems - 1)).wg0;
-    ii = __popcll(__ballot(lane >= 1 && lane < a_n_items && wg >= w0));
-    lds_item_t& it = item_at(tab, ii);
-    it_k = uni(it.k);
-    it_v = uni(it.v);
-    it_q = uni(it.q);
-    it_out = uni(it.out);
-    k_s1 = uni(it.k_s1);
-    v_s1 = uni(it.v_s1);
-    q_s1 = uni(it.q_s1);
-    o_s1 = uni(it.o_s1);
-    n_kv = uni(it.n_kv);
-    kpg = uni(it.kpg);
-    wg0 = uni(it.wg0);
-    ks2 = (int)uni(it.k_s2);
-    vs2 = (int)uni(it.v_s2);
   }
   const int local = wg - wg0;
   const int gl = local / kpg, part = local - gl * kpg;
@@ -446,10 +389,20 @@ void decode_kernel(const DecodeParams p) {
   __attribute__((address_space(3))) unsigned* const take =
       reinterpret_cast<__attribute__((address_space(3))) unsigned*>(lds + C::L_FLAG + 4);
   // Local takes: the workgroup's t-th sub-tile is part + kpg t.
+  // Deterministic launches: wave wv takes the workgroup's sub-tiles wv,
+  // wv + NWV, ... in turn instead, so which wave accumulates which sub-tile,
+  // and with it every rounding, is the same on every run.
+  int seq = wv;
   auto lds_take = [&]() __attribute__((always_inline)) {
     unsigned t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(take, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    t = min((unsigned)__builtin_amdgcn_readfirstlane((int)t), (unsigned)nsub);
+    if (a_det) {
+      t = (unsigned)seq;
+      seq += NWV;
+    } else {
+      if (lane == 0) t = __hip_atomic_fetch_add(take, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
+    }
+    t = min(t, (unsigned)nsub);
     return (int)min((unsigned)part + (unsigned)kpg * t, (unsigned)nsub);
   };
   auto refill = [&](auto slc, bool first) __attribute__((always_inline)) {
@@ -965,23 +918,26 @@ constexpr int decode_waves() {
 }
 
 template <int D, typename KT, int HS, bool DYN>
-static hipError_t launch_decode_t(const DecodeParams& p, hipStream_t stream) {
+static hipError_t launch_decode_t(const DecodeParams& p, int grid_x, int n_items, hipStream_t stream) {
   constexpr int NWV = decode_waves<D, KT>();
   typedef DecodeCfg<D, KT, HS, NWV, DYN> C;
   static const hipError_t attr =
       hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, KT, HS, NWV, DYN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, C::L_TOTAL);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV, DYN>), dim3((unsigned)p.n_wg), dim3(NWV * kWave),
+  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV, DYN>), dim3((unsigned)grid_x, (unsigned)n_items), dim3(NWV * kWave),
                      C::L_TOTAL, stream, p);
   return hipGetLastError();
 }
 
 template <int D, typename KT>
-static hipError_t launch_decode_h(const DecodeParams& p, int group, bool dyn, hipStream_t stream) {
+static hipError_t launch_decode_h(const DecodeParams& p, int grid_x, int n_items, int group, bool dyn,
+                                  hipStream_t stream) {
   if (group > 4)
-    return dyn ? launch_decode_t<D, KT, 2, true>(p, stream) : launch_decode_t<D, KT, 2, false>(p, stream);
-  return dyn ? launch_decode_t<D, KT, 1, true>(p, stream) : launch_decode_t<D, KT, 1, false>(p, stream);
+    return dyn ? launch_decode_t<D, KT, 2, true>(p, grid_x, n_items, stream)
+               : launch_decode_t<D, KT, 2, false>(p, grid_x, n_items, stream);
+  return dyn ? launch_decode_t<D, KT, 1, true>(p, grid_x, n_items, stream)
+             : launch_decode_t<D, KT, 1, false>(p, grid_x, n_items, stream);
 }
 
 int decode_wg_waves(int head_dim, bool f16) {
@@ -1015,14 +971,15 @@ size_t decode_record_floats(int head_dim, int group) {
   return (size_t)(2 * hsl * (head_dim + 2));  // room for the early protocol's 64-bit words
 }
 
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, bool dyn,
-                         hipStream_t stream) {
+hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,
+                         bool dyn, hipStream_t stream) {
+  if (grid_x < 1 || n_items < 1 || n_items > kDecodeMaxItems) return hipErrorInvalidValue;
   if (head_dim == 64)
-    return f16 ? launch_decode_h<64, _Float16>(p, group, dyn, stream)
-               : launch_decode_h<64, float>(p, group, dyn, stream);
+    return f16 ? launch_decode_h<64, _Float16>(p, grid_x, n_items, group, dyn, stream)
+               : launch_decode_h<64, float>(p, grid_x, n_items, group, dyn, stream);
   if (head_dim == 128)
-    return f16 ? launch_decode_h<128, _Float16>(p, group, dyn, stream)
-               : launch_decode_h<128, float>(p, group, dyn, stream);
+    return f16 ? launch_decode_h<128, _Float16>(p, grid_x, n_items, group, dyn, stream)
+               : launch_decode_h<128, float>(p, grid_x, n_items, group, dyn, stream);
   return hipErrorInvalidValue;
 }
 

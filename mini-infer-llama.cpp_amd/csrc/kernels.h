@@ -20,8 +20,10 @@ int decode_team(int head_dim, bool f16, int group);     // workgroups per combin
 // launch's epoch parity is zero on entry; the other is cleared). dyn: the
 // waves claim sub-tiles from the group counters (required when any item has
 // kpg > 1); otherwise each workgroup takes its group's sub-tiles from LDS.
-hipError_t launch_decode(const DecodeParams& p, int head_dim, bool f16, int group, bool dyn,
-                         hipStream_t stream);
+// Grid (grid_x, n_items): row y serves p.item[y]; workgroups past an item's
+// gpi * kpg leave at once.
+hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,
+                         bool dyn, hipStream_t stream);
 // n words at p set to v on `stream` (a kernel, so it may sit in a graph).
 hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t stream);
 

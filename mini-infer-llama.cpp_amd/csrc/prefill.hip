@@ -7,9 +7,10 @@
 // workgroup has the same number of tiles (NQ + 1 + 2 n_past / 32 when the
 // blocks are full). Its NW waves work through that list of (block, tile)
 // units: wave w starts with unit w and then takes units in order from an LDS
-// counter, so a wave that is served faster takes more; a wave's units cross
-// from block i to block NQ - 1 - i at most once, where it parks its first
-// block's partial result in LDS.
+// counter, so a wave that is served faster takes more (or, in deterministic
+// launches, units w + NW, w + 2 NW, ...); a wave's units cross from block i to
+// block NQ - 1 - i at most once, where it parks its first block's partial
+// result in LDS.
 //
 // Per unit (lane = (c = lane % 32, kh = lane / 32)):
 //   1. the key tile's 32 K rows come into the wave's LDS tile by buffer_load
@@ -244,7 +245,16 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     }
   }
   __syncthreads();
+  // The next unit: from the LDS counter, or (deterministic launches) the
+  // wave's fixed sequence wave + NW, wave + 2 NW, ..., so that which wave
+  // computes which unit, and with it every rounding, is the same on every run.
+  int seq = wave;
+  const int det = __builtin_amdgcn_readfirstlane(p.det);
   auto take = [&]() __attribute__((always_inline)) {
+    if (det) {
+      seq += NW;
+      return seq;
+    }
     unsigned t = 0;
     if (lane == 0) t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     return __builtin_amdgcn_readfirstlane((int)t);

@@ -76,6 +76,7 @@ struct State {
   std::atomic<uint64_t> limit{0};
   int n_cu = 0;  // compute units of the device
   Knobs knobs;
+  std::atomic<int> deterministic{1};  // fixed per-wave takes in the fused kernels
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
   mi_hip_workspace* scratch_ws = nullptr;  // over the static scratch array (never freed)
 };
@@ -132,8 +133,8 @@ constexpr float kLog2e = 1.4426950408889634f;
 // kpg-th sub-tile of its group.
 struct DecodePlan {
   int group = 1, n_chunks = 1;
-  int n_wg = 0;
-  int uniform_kpg = 0;  // every item's kpg when they agree, else 0
+  int n_wg = 0;    // workgroups with work (records)
+  int grid_x = 0;  // the widest item's workgroups (grid rows are items)
   bool dyn = false;     // dynamic sub-tile claims
 };
 
@@ -160,11 +161,10 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
     it[i].kpg = (int32_t)k;
     it[i].wg0 = (int32_t)wg;
     wg += (int64_t)gpi * k;
-    if (k > 1 && g.knobs.claim > 0 && it[i].spg >= (int64_t)g.knobs.claim * k * ring) p.dyn = true;
+    if (k > 1 && g.knobs.claim > 0 && it[i].spg >= (int64_t)g.knobs.claim * k * ring && !g.deterministic)
+      p.dyn = true;
   }
-  p.uniform_kpg = it[0].kpg;
-  for (int i = 1; i < n_items; ++i)
-    if (it[i].kpg != it[0].kpg) p.uniform_kpg = 0;
+  for (int i = 0; i < n_items; ++i) p.grid_x = std::max(p.grid_x, gpi * it[i].kpg);
   p.n_wg = (int)wg;
   return p;
 }
@@ -466,25 +466,24 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
                   "decode launch of %d groups and %zu record bytes exceeds its workspace (%d groups, "
                   "%zu bytes): create the workspace for this head shape",
                   cnt * gpi, rec_bytes, ws->groups, ws->rec_bytes);
-    p.n_items = cnt;
     p.n_rep = items[0].n_rep;
     p.n_head_kv = r0.n_head_kv;
     p.n_chunks = plan.n_chunks;
     p.gpi = gpi;
     p.n_wg = plan.n_wg;
-    p.uniform_kpg = plan.uniform_kpg;
     p.scale_log2e = items[0].scale * kLog2e;
     p.rec = ws->rec;
     p.cnt = ws->cnt;
     p.status = ws->status;
     p.ctr_groups = ws->groups;
     p.max_polls = ws->max_polls;
+    p.det = g.deterministic.load();
     // The early merge is worth its wait when every workgroup of the launch can
     // be resident at once (one per CU); it stays correct otherwise.
     // (knob 2 forces it: tests of the fallback for parts that start late).
     p.early = g.knobs.early == 2 || (plan.n_wg <= g.n_cu && g.knobs.early != 0);
     if ((rc = ws_next_epoch(ws, cnt * gpi, stream, &p.epoch, &p.clear_groups))) return rc;
-    hipError_t e = mi::launch_decode(p, r0.head_dim, r0.f16, plan.group, plan.dyn, stream);
+    hipError_t e = mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     base += cnt;
   }
@@ -520,6 +519,7 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   p.n_tokens = a->n_tokens;
   p.n_qblocks = (a->n_tokens + mi::kPrefillRows - 1) / mi::kPrefillRows;
   p.scale_log2e = a->scale * kLog2e;
+  p.det = g.deterministic.load();
   hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, g.n_cu, stream);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   return MI_HIP_OK;
@@ -911,6 +911,12 @@ int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim
   if (early >= 0) g.knobs.early = early;
   if (solo >= 0) g.knobs.solo = solo;
   if (claim >= 0) g.knobs.claim = claim;
+  return MI_HIP_OK;
+}
+
+int mi_hip_set_deterministic(int32_t on) {
+  if (on != 0 && on != 1) return fail(MI_HIP_E_INVALID, "on must be 0 or 1");
+  g.deterministic.store(on);
   return MI_HIP_OK;
 }
 

@@ -106,10 +106,13 @@ def test_decode_f16_cache_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv):
 @pytest.fixture()
 def tuning(hip):
     """Sets decode planner knobs for one test and restores the defaults."""
-    def set_(kpg=-1, early=-1, solo=-1, claim=-1):
+    def set_(kpg=-1, early=-1, solo=-1, claim=-1, det=None):
         hip.check(hip.mi_hip_decode_tuning(kpg, early, solo, claim))
+        if det is not None:
+            hip.check(hip.mi_hip_set_deterministic(det))
     yield set_
     hip.check(hip.mi_hip_decode_tuning(0, 1, 1, 0))
+    hip.check(hip.mi_hip_set_deterministic(1))
 
 
 # Forced workgroups per group: the early protocol (2..8 parts, with and without
@@ -119,15 +122,68 @@ def tuning(hip):
 @pytest.mark.parametrize("d,f16", [(64, False), (128, True)])
 @pytest.mark.parametrize("claim", [1, 0])
 def test_decode_forced_split(hip, stream, oracle, tuning, kpg, early, d, f16, claim):
-    # claim 1: sub-tiles claimed from the group counter; 0: every kpg-th sub-tile per part
+    # claim 1: sub-tiles claimed from the group counter (dynamic takes, which
+    # the deterministic mode turns off); 0: every kpg-th sub-tile per part,
+    # in fixed (deterministic) order
     print("forced split", kpg, early, d, f16, claim, flush=True)
-    tuning(kpg=kpg, early=early, claim=claim)
+    tuning(kpg=kpg, early=early, claim=claim, det=0 if claim else 1)
     n_kv = 3000 + 20 * kpg  # long enough that the forced split is not capped below 33 parts
     hkv = 2 if d == 64 else 4
     q, k, v = cpu_attention.make_inputs(4100 + kpg + d, d, 7 * hkv, hkv, n_kv, 1)
     scale = float(np.float32(1) / np.sqrt(np.float32(d)))
     got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=f16)
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=f16), TOL_F32)
+
+
+@pytest.fixture()
+def deterministic(hip):
+    """Deterministic fused kernels (the library default) for one test."""
+    hip.check(hip.mi_hip_set_deterministic(1))
+    yield
+    hip.check(hip.mi_hip_set_deterministic(1))
+
+
+@pytest.fixture()
+def dynamic_takes(hip):
+    """The non-deterministic (counter-taking) fused kernels for one test."""
+    hip.check(hip.mi_hip_set_deterministic(0))
+    yield
+    hip.check(hip.mi_hip_set_deterministic(1))
+
+
+@pytest.mark.parametrize("kpg", [0, 3, 8, 24])
+def test_deterministic_decode_repeats_bit_for_bit(hip, stream, oracle, tuning, deterministic, kpg):
+    # With fixed per-wave takes every merge runs in a fixed order, so five
+    # launches of one problem give the same bits (planned split and forced
+    # splits over both merge protocols), and they meet the oracle's bar.
+    tuning(kpg=kpg)
+    n_kv = 4096 + 77
+    q, k, v = cpu_attention.make_inputs(6060 + kpg, 64, 14, 2, n_kv, 1)
+    runs = [fused(hip, stream, q, k, v, n_kv - 1, 0.125) for _ in range(5)]
+    for i, r in enumerate(runs[1:]):
+        assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32)), f"run {i + 1}"
+    assert_close(runs[0], ref_out(oracle, q, k, v, n_kv - 1, 0.125), TOL_F32)
+
+
+def test_prefill_dynamic_takes(hip, stream, oracle, dynamic_takes):
+    # the counter-taking prefill (deterministic mode off) against the oracle
+    n = 1024
+    q, k, v = cpu_attention.make_inputs(6262, 64, 14, 2, n, n)
+    got = fused(hip, stream, q, k, v, 0, 0.125)
+    for j in (0, 33, 640, 1023):
+        want = oracle.attention(q[j:j + 1], k, v, j, 0.125, 8)[2]
+        assert_close(got[j:j + 1], want, TOL_F32, f"row {j}")
+
+
+def test_deterministic_prefill_repeats_bit_for_bit(hip, stream, oracle, deterministic):
+    n = 1024
+    q, k, v = cpu_attention.make_inputs(6161, 64, 14, 2, n, n)
+    runs = [fused(hip, stream, q, k, v, 0, 0.125) for _ in range(3)]
+    for i, r in enumerate(runs[1:]):
+        assert np.array_equal(r.view(np.uint32), runs[0].view(np.uint32)), f"run {i + 1}"
+    for j in (0, 31, 500, 1023):
+        want = oracle.attention(q[j:j + 1], k, v, j, 0.125, 8)[2]
+        assert_close(runs[0][j:j + 1], want, TOL_F32, f"row {j}")
 
 
 def test_decode_back_to_back_launches_share_no_records(hip, stream, oracle):
@@ -268,12 +324,13 @@ def test_two_workspaces_decode_concurrently(hip, oracle):
         hip.check(hip.mi_hip_workspace_destroy(w2))
 
 
+@pytest.mark.parametrize("det", [1, 0])
 @pytest.mark.parametrize("early", [1, 0])
-def test_decode_batch_24_layers(hip, stream, oracle, tuning, early):
+def test_decode_batch_24_layers(hip, stream, oracle, tuning, early, det):
     # both cross-workgroup combines at the headline shape (5 workgroups per
     # group): the first finisher polling stamped records, and the counters
     import torch
-    tuning(early=early)
+    tuning(early=early, det=det)
     n_layers, n_kv = 24, 4096
     qs, ks, vs, outs, items = [], [], [], [], []
     for layer in range(n_layers):
