@@ -258,7 +258,7 @@ def bench_e2e(mh):
     the reference-order mode's ids are checked against the reference engine's."""
     import tempfile
     import qwen2_gguf as gg
-    from qwen2 import Qwen2
+    from qwen2 import Qwen2, fork_summary, teacher_forced
     d = tempfile.mkdtemp(prefix="mi_e2e_")
     path = os.path.join(d, "qwen05_q8_0.gguf")
     sha = gg.write_qwen2_q8_0(path, E2E_SEED)
@@ -268,6 +268,7 @@ def bench_e2e(mh):
     out = {"workload": "Qwen2.5-0.5B-shaped random-init Q8_0 GGUF (seed 1234), 128-token prompt, "
                        "256 greedy ids (1 prefill + 255 decode calls), n_ctx 2048",
            "model_sha256_ok": sha == gold["model_sha256"]}
+    free = {}
     with Qwen2(path, n_ctx=2048, max_tokens=len(prompt)) as m:
         for mode, key in ((mh.MI_HIP_QWEN2_ATTN_FUSED, "fused"),
                           (mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER, "reference_order")):
@@ -298,6 +299,19 @@ def bench_e2e(mh):
                         "ids_equal_reference": ids == gold["ids"],
                         "ids_agree_steps": next((i for i, (a, b) in enumerate(zip(ids, gold["ids"]))
                                                  if a != b), len(ids))}
+            free[key] = ids
+        # the fused engine in lockstep with the reference-order one under
+        # teacher forcing: where and by how much its argmax flips
+        m.set_attention(mh.MI_HIP_QWEN2_ATTN_FUSED)
+        with Qwen2(path, n_ctx=2048, max_tokens=len(prompt)) as ref:
+            ref.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
+            recs = teacher_forced(m, ref, prompt, gold["ids"])
+        summ = fork_summary(recs, free["fused"], gold["ids"])
+        summ["reference_order_argmax_equal_reference"] = [r["ref_id"] for r in recs] == gold["ids"]
+        summ["flips_are_near_ties"] = all(r["margin"] <= 2 * r["max_diff"] for r in recs
+                                          if r["fused_id"] != r["ref_id"])
+        out["fused"]["teacher_forced"] = {k: (round(v, 5) if isinstance(v, float) else v)
+                                          for k, v in summ.items()}
     return out, path, d
 
 

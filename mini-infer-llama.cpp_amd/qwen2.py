@@ -87,6 +87,51 @@ class Qwen2:
         return out
 
 
+def teacher_forced(fused, ref, prompt, ids):
+    """Runs two engines in lockstep on the same history -- the prompt, then
+    ids[0..i) one token per call (teacher forcing) -- and compares each step's
+    last-position logits. Returns one record per step i (the logits that pick
+    ids[i]): the reference engine's argmax and its top-1/top-2 margin, the
+    other engine's argmax, and the largest logit difference. This is the fork
+    classification of the reference's own divergence analysis
+    (docs/stage1.md:118-132): a step where the argmaxes differ is a near-tie
+    when its margin is within the logit differences, not a wrong history."""
+    import numpy as np
+
+    def step(tokens, n_past):
+        out = []
+        for m in (fused, ref):
+            _, logits = m.forward(tokens, n_past=n_past, want_logits=True)
+            out.append(np.frombuffer(logits, dtype=np.float32).copy())
+        return out
+
+    recs = []
+    for i in range(len(ids)):
+        lf, lr = step(prompt, 0) if i == 0 else step([ids[i - 1]], len(prompt) + i - 1)
+        top2 = np.argpartition(lr, -2)[-2:]
+        a, b = (top2[0], top2[1]) if lr[top2[0]] >= lr[top2[1]] else (top2[1], top2[0])
+        recs.append(dict(step=i, ref_id=int(np.argmax(lr)), fused_id=int(np.argmax(lf)),
+                         margin=float(lr[a] - lr[b]), max_diff=float(np.abs(lf - lr).max())))
+    return recs
+
+
+def fork_summary(recs, free_running_ids, ref_ids):
+    """The numbers that classify the forks of a free-running generation
+    against the reference's ids, from teacher_forced records."""
+    flips = [r for r in recs if r["fused_id"] != r["ref_id"]]
+    first = next((i for i, (a, b) in enumerate(zip(free_running_ids, ref_ids)) if a != b), None)
+    out = dict(steps=len(recs), teacher_forced_flips=len(flips),
+               flip_steps=[r["step"] for r in flips],
+               largest_margin_at_flip=max((r["margin"] for r in flips), default=None),
+               max_logit_diff=max(r["max_diff"] for r in recs),
+               median_margin=sorted(r["margin"] for r in recs)[len(recs) // 2],
+               first_free_running_divergence=first)
+    if first is not None and first < len(recs):
+        out["margin_at_first_divergence"] = recs[first]["margin"]
+        out["max_logit_diff_at_first_divergence"] = recs[first]["max_diff"]
+    return out
+
+
 def read_ids(path):
     with open(path) as f:
         return [int(t) for t in f.read().split()]
