@@ -45,7 +45,7 @@ def parse():
     ap.add_argument("--deterministic", action="store_true",
                     help="fixed per-wave takes in the fused kernels (mi_hip_set_deterministic)")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
+                    help="comma list: decode,sweep,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
                          "counter calibration workload, only when named)")
     return ap.parse_args()
 
@@ -332,46 +332,96 @@ def cpu_reference_engine(path, prompt_path, threads=16):
             "kind": "reference"}
 
 
+def cpu_share():
+    """Host cores this process may use on the box: its affinity set, capped at
+    the 16 cores a one-GPU box grants a job (its OMP_NUM_THREADS)."""
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except OSError:
+        allowed = os.cpu_count() or 1
+    return max(1, min(allowed, int(os.environ.get("OMP_NUM_THREADS", "16") or 16), 16))
+
+
+def cpu_info():
+    """The host CPU: model string, logical CPUs (nproc), physical cores."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    return dict(cpu=model, nproc=os.cpu_count() or 1, physical_cores=len(cores) or None)
+
+
 def cpu_baseline(n_layers_sample=24, n_kv=4096, target_s=12.0):
-    """The reference three-node CPU path on the host cores, on a bounded sample
-    of the decode workload: 24 layers' decode attention at n_kv = 4096, passes
-    repeated until about `target_s` seconds of CPU work (median pass), then
+    """The reference three-node CPU path (attn_qk -> softmax -> attn_kqv as
+    graph nodes on its own thread pool) on the host cores, on a bounded sample
+    of the decode workload: 24 layers' decode attention at n_kv = 4096. Thread
+    counts 1, 2, 4, ... up to the job's CPU share are swept as the reference's
+    scripts/bench_threads.py sweeps them (1 warmup, median of 5); the best is
+    then timed over about `target_s` seconds of CPU work (median pass), and
     prefill-1024 a few times."""
     import numpy as np
     from oracle import cpu_attention
     impl = cpu_attention.reference() or cpu_attention.oracle()
-    threads = min(os.cpu_count() or 1, 16)
+    share = cpu_share()
     rng = np.random.default_rng(7)
     qs = [rng.standard_normal((1, 14, 64), dtype=np.float32) for _ in range(n_layers_sample)]
     ks = [rng.standard_normal((n_kv, 2, 64), dtype=np.float32) for _ in range(n_layers_sample)]
     vs = [rng.standard_normal((n_kv, 2, 64), dtype=np.float32) for _ in range(n_layers_sample)]
+    nbytes = decode_bytes(n_layers_sample, n_kv, 14, 2, 64, 4)
+    counts = sorted({min(1 << i, share) for i in range(6)} | {share})
+    sweep = {}
+    for t in counts:
+        ts, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, t, warmup=1, reps=5)
+        sweep[t] = nbytes / ts / 1e9
+    threads = max(sweep, key=sweep.get)
     t0, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, threads, warmup=1, reps=3)
     reps = int(min(5000, max(7, target_s / max(t0, 1e-6))))
     t, _ = impl.time_attention(qs, ks, vs, n_kv - 1, 0.125, threads, warmup=0, reps=reps)
-    nbytes = decode_bytes(n_layers_sample, n_kv, 14, 2, 64, 4)
     # prefill-1024 on the CPU (the reference computes every key, masked or
     # not; the FLOP count below is still the causal one)
     q = rng.standard_normal((1024, 14, 64), dtype=np.float32)
     k = rng.standard_normal((1024, 2, 64), dtype=np.float32)
     v = rng.standard_normal((1024, 2, 64), dtype=np.float32)
     tp, _ = impl.time_attention([q], [k], [v], 0, 0.125, threads, warmup=1, reps=5)
+    info = cpu_info()
     return dict(value=nbytes / t / 1e9, unit="GB/s", cores=threads, kind=impl.kind,
                 sample=f"24 layers x decode n_kv=4096 (14 Q / 2 KV heads, head_dim 64, F32), "
-                       f"median of {reps} passes ({reps * t:.1f} s); attn_qk -> softmax -> "
-                       f"attn_kqv, barrier per node, static (head,row) split",
+                       f"median of {reps} passes ({reps * t:.1f} s) at the best thread count; "
+                       f"attn_qk -> softmax -> attn_kqv, barrier per node, static (head,row) split",
                 us_per_layer=t * 1e6 / n_layers_sample,
                 prefill1024_s=tp, prefill1024_tflops=causal_flops(1024, 14, 64) / tp / 1e12,
-                cpu=_cpu_model())
+                threads_sweep_gbps={str(k): round(v, 3) for k, v in sweep.items()},
+                best_threads=threads, cpu_share=share, **info)
 
 
-def _cpu_model():
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    return "unknown"
+def measured_mfma():
+    """MFMA utilisation of the prefill kernel from the committed rocprofv3
+    counter summary (profiles/prefill_f32_mfma.txt)."""
+    p = os.path.join(ROOT, "profiles", "prefill_mfma.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        m = json.load(f)
+    keep = ("kernel_us", "mfma_util_of_spec", "mfma_util_at_measured_clock", "executed_over_causal",
+            "executed_tflops", "mfma_f32_insts")
+    return {"source": "profiles/prefill_f32_mfma.txt (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F32)",
+            "measured_shader_clock_ghz": m.get("measured_shader_clock_ghz"),
+            **{f"n{n}": {k: m[n][k] for k in keep if k in m[n]} for n in ("1024", "4096") if n in m}}
 
 
 def measured_traffic(name="decode_traffic.json"):
@@ -405,6 +455,18 @@ def main():
         res["decode"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
         print(f"# decode 24x4096: {res['decode']['gbps']:.1f} GB/s per step, kernel "
               f"{res['decode']['kernel_gbps']:.1f} GB/s", file=sys.stderr, flush=True)
+    if want("sweep"):
+        res["sweep"] = {}
+        for n_kv in (128, 1024, 4096, 16384, 32768):
+            st = max(20, min(args.steps, 8_000_000 // (n_kv * 24)))
+            res["sweep"][n_kv] = (res["decode"] if n_kv == 4096 and "decode" in res else
+                                  bench_decode(torch, mh, lib, stream, st, max(2, st // 10), n_kv=n_kv))
+            print(f"# decode 24x{n_kv}: {res['sweep'][n_kv]['kernel_gbps']:.1f} GB/s, "
+                  f"{res['sweep'][n_kv]['kernel_ms'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+        res["config1"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup, n_layers=1,
+                                      n_kv=512)
+        print(f"# decode 1 layer x 512: {res['config1']['kernel_ms'] * 1e3:.2f} us", file=sys.stderr,
+              flush=True)
     if want("prefill"):
         res["prefill1024"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
         res["prefill4096"] = bench_prefill(torch, mh, lib, stream, max(10, args.steps // 10),
@@ -521,8 +583,23 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(p1["tflops"], 2),
                          "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(p1["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
-                         "flops_per_launch": p1["flops"]},
+                         "flops_per_launch": p1["flops"], "mfma_counters": measured_mfma()},
         }
+    if "sweep" in res:
+        out["decode_sweep"] = {
+            "workload": "24 independent layer caches, 1 query token, 14 Q / 2 KV heads, head_dim 64, "
+                        "F32 K/V, one batched launch per step, cache sets rotated beyond the MALL",
+            "by_n_kv": {str(n): {"us": round(r["kernel_ms"] * 1e3, 3), "us_per_layer":
+                                 round(r["kernel_ms"] * 1e3 / 24, 3), "gbps": round(r["kernel_gbps"], 1),
+                                 "frac": round(r["kernel_gbps"] / HBM_PEAK_GBPS, 4),
+                                 "bytes": r["bytes"], "cache_sets": r["sets"]}
+                        for n, r in res["sweep"].items()}}
+        c1 = res["config1"]
+        out["decode_config1"] = {
+            "workload": "one layer, n_kv 512, 14 Q / 2 KV heads, head_dim 64, F32 K/V (the reference's "
+                        "CPU-runnable case)",
+            "us_per_layer": round(c1["kernel_ms"] * 1e3, 3), "gbps": round(c1["kernel_gbps"], 1),
+            "frac": round(c1["kernel_gbps"] / HBM_PEAK_GBPS, 4), "bytes": c1["bytes"]}
     if "decode7b" in res:
         r = res["decode7b"]
         out["decode_7b_f16"] = {"n_kv": 8192, "gbps": round(r["kernel_gbps"], 1),
