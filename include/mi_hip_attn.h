@@ -144,6 +144,19 @@ int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim
  * construction: src/ops_cpu.cpp:38-53). */
 int mi_hip_set_deterministic(int32_t on);
 
+/* Matrix cores of the prefill kernel's QK and PV products.
+ *   MI_HIP_PREFILL_SPLIT_BF16 (the default): every float operand is split
+ *     into a pair of bf16 (hi = round(x), lo = round(x - hi), |x - hi - lo| <=
+ *     2^-17 |x|) and each product is lo.hi + hi.lo + hi.hi on
+ *     v_mfma_f32_32x32x16_bf16 with float accumulation: ~1e-5 relative per
+ *     product, three bf16 products at 16x the FP32 matrix rate.
+ *   MI_HIP_PREFILL_F32: v_mfma_f32_32x32x2f32 (float products).
+ * Both are within the 1e-4 bar of the reference ops. Process-wide. No
+ * counterpart in the reference. */
+#define MI_HIP_PREFILL_F32 0
+#define MI_HIP_PREFILL_SPLIT_BF16 1
+int mi_hip_set_prefill_mode(int32_t mode);
+
 /* ---- device-resident KV cache ------------------------------------------ */
 
 typedef struct mi_hip_kv mi_hip_kv;

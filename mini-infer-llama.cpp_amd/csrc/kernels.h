@@ -27,8 +27,10 @@ hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int hea
 // n words at p set to v on `stream` (a kernel, so it may sit in a graph).
 hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t stream);
 
-// prefill.hip
-hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu,
+// prefill.hip. split: the QK and PV products on the bf16 matrix cores with
+// operands split into hi + lo bf16 pairs (three products each); otherwise
+// v_mfma_f32_32x32x2f32.
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu, bool split,
                           hipStream_t stream);
 
 // nodes.hip -- node-level kernels on device tensors (byte strides).

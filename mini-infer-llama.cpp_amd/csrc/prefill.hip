@@ -43,6 +43,7 @@
 namespace mi {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) f32x4 lds_f32x4;
@@ -94,6 +95,27 @@ __device__ inline float xor32_sum(float x) {
   return a + b;
 }
 
+// Eight floats as hi + lo bf16 pairs: hi = bf16(x) rounded to nearest even,
+// lo = bf16(x - hi) (x - hi is exact in float), so |x - hi - lo| <= 2^-17 |x|.
+__device__ inline void split8(const float* x, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const __bf16 h = (__bf16)x[i];
+    hi[i] = h;
+    lo[i] = (__bf16)(x[i] - (float)h);
+  }
+}
+
+// acc += a . b over 16 k-values with float inputs split into bf16 pairs:
+// a_lo.b_hi + a_hi.b_lo + a_hi.b_hi (the a_lo.b_lo term, below 2^-18 of the
+// product, is dropped), three v_mfma_f32_32x32x16_bf16 in that order.
+__device__ inline floatx16 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl,
+                                 floatx16 acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh, acc, 0, 0, 0);
+}
+
 }  // namespace
 
 template <int D, typename KT, int NW>
@@ -128,7 +150,7 @@ struct PrefillCfg {
   static_assert(LDS <= 160 * 1024, "LDS budget");
 };
 
-template <int D, typename KT, int NW>
+template <int D, typename KT, int NW, bool SPLIT>
 __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams p) {
   typedef PrefillCfg<D, KT, NW> C;
   constexpr int HALF = C::HALF, NDB = C::NDB, NV = C::NV, RS = C::RS, ELT = C::ELT;
@@ -314,11 +336,32 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     }
   };
 
-  // S^T = K . Q^T
+  // The block's queries as bf16 pairs (SPLIT): step s, item i holds dim
+  // kh HALF + 8 s + i, the dims of kk[8 s + i] (any pairing of the k-values
+  // is a valid contraction as long as A and B agree).
+  bf16x8 qh[SPLIT ? HALF / 8 : 1], ql[SPLIT ? HALF / 8 : 1];
+  auto split_q = [&]() __attribute__((always_inline)) {
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int st = 0; st < HALF / 8; ++st) split8(qb + 8 * st, qh[st], ql[st]);
+    }
+  };
+
+  // S^T = K . Q^T: D/2 v_mfma_f32_32x32x2f32, or (SPLIT) D/16 steps of three
+  // v_mfma_f32_32x32x16_bf16 on bf16-pair-split operands
   auto qk = [&](const float (&kk)[HALF]) __attribute__((always_inline)) {
     floatx16 s = (floatx16)(0.f);
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int st = 0; st < HALF; ++st) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[st], qb[st], s, 0, 0, 0);
+      for (int st = 0; st < HALF / 8; ++st) {
+        bf16x8 kh8, kl8;
+        split8(kk + 8 * st, kh8, kl8);
+        s = mfma3(kh8, kl8, qh[st], ql[st], s);
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < HALF; ++st) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[st], qb[st], s, 0, 0, 0);
+    }
     return s;
   };
 
@@ -349,13 +392,36 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     m = mn;
   };
 
-  // O^T += V^T . P^T
+  // O^T += V^T . P^T: 16 v_mfma_f32_32x32x2f32 per 32 output dims, or (SPLIT)
+  // two steps of three v_mfma_f32_32x32x16_bf16, step u taking registers
+  // 8u .. 8u + 7 of S^T (keys 8 (r / 4) + 4 kh + r % 4) and the V values of
+  // the same keys
   auto pv = [&](const floatx16& s, const float (&vv)[NV]) __attribute__((always_inline)) {
+    if constexpr (SPLIT) {
 #pragma unroll
-    for (int t = 0; t < 16; ++t)
+      for (int u = 0; u < 2; ++u) {
+        float pf[8];
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t * NDB + db], s[t], o[db], 0, 0, 0);
+        for (int i = 0; i < 8; ++i) pf[i] = s[8 * u + i];
+        bf16x8 ph, pl;
+        split8(pf, ph, pl);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          float vf[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) vf[i] = vv[(8 * u + i) * NDB + db];
+          bf16x8 vh, vl;
+          split8(vf, vh, vl);
+          o[db] = mfma3(vh, vl, ph, pl, o[db]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 16; ++t)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t * NDB + db], s[t], o[db], 0, 0, 0);
+    }
   };
 
   // The wave's units, software-pipelined (see the header). Request order per
@@ -366,6 +432,7 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   int u = wave;
   if (u < T) {
     load_q(blk(u));
+    split_q();
     reset(blk(u));
     wait_vmem<0>();
     read_k(kk);
@@ -379,7 +446,10 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       // sc: scores of unit u; the LDS tile is filling with unit un's K
       const int unn = take();
       const int Xu = blk(u), Xn = blk(un);
-      if (Xn != Xu) load_q(Xn);  // the running state still belongs to Xu
+      if (Xn != Xu) {  // the running state still belongs to Xu
+        load_q(Xn);
+        split_q();
+      }
       wait_vmem<C::WAIT_K>();
       read_k(kk);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the whole A operand at once
@@ -482,27 +552,34 @@ static int prefill_choose_lone(const PrefillParams& p, int n_cu) {
   return best_lone;
 }
 
-template <int D, typename KT>
+template <int D, typename KT, bool SPLIT>
 static hipError_t launch_prefill_t(PrefillParams p, int n_cu, hipStream_t stream) {
   constexpr int NW = prefill_waves<D>();
   typedef PrefillCfg<D, KT, NW> C;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<D, KT, NW>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<D, KT, NW, SPLIT>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
   if (attr != hipSuccess) return attr;
   p.lone = prefill_choose_lone(p, n_cu);
   const unsigned per_head = (unsigned)prefill_wgs_per_head(p.n_qblocks, p.lone);
-  hipLaunchKernelGGL((prefill_kernel<D, KT, NW>), dim3((unsigned)p.n_head * per_head),
+  hipLaunchKernelGGL((prefill_kernel<D, KT, NW, SPLIT>), dim3((unsigned)p.n_head * per_head),
                      dim3(NW * kWave), C::LDS, stream, p);
   return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu, hipStream_t stream) {
+template <int D, typename KT>
+static hipError_t launch_prefill_m(const PrefillParams& p, int n_cu, bool split, hipStream_t stream) {
+  return split ? launch_prefill_t<D, KT, true>(p, n_cu, stream) : launch_prefill_t<D, KT, false>(p, n_cu, stream);
+}
+
+hipError_t launch_prefill(const PrefillParams& p, int head_dim, bool f16, int n_cu, bool split,
+                          hipStream_t stream) {
   if (head_dim == 64)
-    return f16 ? launch_prefill_t<64, _Float16>(p, n_cu, stream) : launch_prefill_t<64, float>(p, n_cu, stream);
+    return f16 ? launch_prefill_m<64, _Float16>(p, n_cu, split, stream)
+               : launch_prefill_m<64, float>(p, n_cu, split, stream);
   if (head_dim == 128)
-    return f16 ? launch_prefill_t<128, _Float16>(p, n_cu, stream)
-               : launch_prefill_t<128, float>(p, n_cu, stream);
+    return f16 ? launch_prefill_m<128, _Float16>(p, n_cu, split, stream)
+               : launch_prefill_m<128, float>(p, n_cu, split, stream);
   return hipErrorInvalidValue;
 }
 

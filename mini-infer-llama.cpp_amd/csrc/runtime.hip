@@ -77,6 +77,7 @@ struct State {
   int n_cu = 0;  // compute units of the device
   Knobs knobs;
   std::atomic<int> deterministic{1};  // fixed per-wave takes in the fused kernels
+  std::atomic<int> prefill_mode{MI_HIP_PREFILL_SPLIT_BF16};  // matrix cores of the prefill kernel
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
   mi_hip_workspace* scratch_ws = nullptr;  // over the static scratch array (never freed)
 };
@@ -520,7 +521,8 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   p.n_qblocks = (a->n_tokens + mi::kPrefillRows - 1) / mi::kPrefillRows;
   p.scale_log2e = a->scale * kLog2e;
   p.det = g.deterministic.load();
-  hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, g.n_cu, stream);
+  hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, g.n_cu,
+                                    g.prefill_mode.load() == MI_HIP_PREFILL_SPLIT_BF16, stream);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   return MI_HIP_OK;
 }
@@ -911,6 +913,13 @@ int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim
   if (early >= 0) g.knobs.early = early;
   if (solo >= 0) g.knobs.solo = solo;
   if (claim >= 0) g.knobs.claim = claim;
+  return MI_HIP_OK;
+}
+
+int mi_hip_set_prefill_mode(int32_t mode) {
+  if (mode != MI_HIP_PREFILL_F32 && mode != MI_HIP_PREFILL_SPLIT_BF16)
+    return fail(MI_HIP_E_INVALID, "prefill mode %d: MI_HIP_PREFILL_F32 (0) or MI_HIP_PREFILL_SPLIT_BF16 (1)", mode);
+  g.prefill_mode.store(mode);
   return MI_HIP_OK;
 }
 

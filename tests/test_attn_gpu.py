@@ -362,8 +362,10 @@ def test_decode_batch_24_layers(hip, stream, oracle, tuning, early, det):
     (0, 500, 128, 28, 4),
     (300, 2, 64, 14, 2),
 ])
-def test_prefill_vs_oracle(hip, stream, oracle, n_past, n_tok, d, h, hkv):
-    print("prefill", n_past, n_tok, d, h, hkv, flush=True)
+@pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_SPLIT_BF16, mh.MI_HIP_PREFILL_F32])
+def test_prefill_vs_oracle(hip, stream, oracle, prefill_mode, mode, n_past, n_tok, d, h, hkv):
+    print("prefill", n_past, n_tok, d, h, hkv, mode, flush=True)
+    prefill_mode(mode)
     q, k, v = cpu_attention.make_inputs(777 + n_tok, d, h, hkv, n_past + n_tok + 3, n_tok)
     scale = float(np.float32(1) / np.sqrt(np.float32(d)))
     got = fused(hip, stream, q, k, v, n_past, scale)
@@ -446,11 +448,24 @@ def test_kv_cache_write_and_attend(hip, stream, oracle, golden_manifest):
             hip.check(hip.mi_hip_kv_destroy(kv))
 
 
-def test_prefill_then_decode_equals_one_prefill(hip, stream):
+@pytest.fixture()
+def prefill_mode(hip):
+    """Sets the prefill kernel's matrix-core mode for one test; the default afterwards."""
+    def set_(mode):
+        hip.check(hip.mi_hip_set_prefill_mode(mode))
+    yield set_
+    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_SPLIT_BF16))
+
+
+@pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_F32, mh.MI_HIP_PREFILL_SPLIT_BF16])
+def test_prefill_then_decode_equals_one_prefill(hip, stream, prefill_mode, mode):
     # The engine's batch-vs-incremental check (tests/test_model_qwen2.cpp:87-134)
     # restated for the attention path: one prefill of T tokens equals a
-    # prefill of the first P followed by T - P single-token decodes.
+    # prefill of the first P followed by T - P single-token decodes. With
+    # float products in both kernels they agree to 2e-6; with the prefill's
+    # bf16-pair products (~1e-5 relative per product) to the parity bar.
     import torch
+    prefill_mode(mode)
     T, P = 70, 50
     q, k, v = cpu_attention.make_inputs(8080, 64, 14, 2, 128, T)
     kv = hip.kv_create(1, 128, 2, 64, 14)
@@ -469,6 +484,7 @@ def test_prefill_then_decode_equals_one_prefill(hip, stream):
             a = mh.attn_args(dq[j:j + 1], parts[j:j + 1], 7, j, 0.125, stream, kv=kv, layer=0)
             hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
         torch.cuda.synchronize()
-        assert_close(parts.cpu().numpy(), whole.cpu().numpy(), dict(atol=2e-6, rtol=2e-6))
+        tol = dict(atol=2e-6, rtol=2e-6) if mode == mh.MI_HIP_PREFILL_F32 else TOL_F32
+        assert_close(parts.cpu().numpy(), whole.cpu().numpy(), tol)
     finally:
         hip.check(hip.mi_hip_kv_destroy(kv))

