@@ -42,8 +42,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--deterministic", action="store_true",
-                    help="fixed per-wave takes in the fused kernels (mi_hip_set_deterministic)")
+    ap.add_argument("--nondeterministic", action="store_true",
+                    help="waves take work from a counter in the fused kernels (mi_hip_set_deterministic(0))")
+    ap.add_argument("--prefill-f32", action="store_true",
+                    help="prefill products on v_mfma_f32_32x32x2f32 instead of split bf16 pairs")
     ap.add_argument("--only", default="",
                     help="comma list: decode,sweep,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
                          "counter calibration workload, only when named)")
@@ -410,18 +412,19 @@ def cpu_baseline(n_layers_sample=24, n_kv=4096, target_s=12.0):
 
 
 def measured_mfma():
-    """MFMA utilisation of the prefill kernel from the committed rocprofv3
-    counter summary (profiles/prefill_f32_mfma.txt)."""
+    """Matrix-core use of the prefill kernel from the committed rocprofv3
+    counter summary (profiles/prefill_mfma.txt): split bf16 pairs at n=1024
+    and 4096, float products at n=1024."""
     p = os.path.join(ROOT, "profiles", "prefill_mfma.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         m = json.load(f)
-    keep = ("kernel_us", "mfma_util_of_spec", "mfma_util_at_measured_clock", "executed_over_causal",
-            "executed_tflops", "mfma_f32_insts")
-    return {"source": "profiles/prefill_f32_mfma.txt (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F32)",
-            "measured_shader_clock_ghz": m.get("measured_shader_clock_ghz"),
-            **{f"n{n}": {k: m[n][k] for k in keep if k in m[n]} for n in ("1024", "4096") if n in m}}
+    keep = ("kernel_us", "mfma_insts", "issued_tflops", "issued_peak_tflops", "issued_frac_of_peak",
+            "mfma_busy_frac", "causal_frac_of_fp32_peak")
+    return {"source": "profiles/prefill_mfma.txt (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16/_F32, "
+                      "kernel trace)",
+            **{k: {f: v[f] for f in keep if f in v} for k, v in m.items()}}
 
 
 def measured_traffic(name="decode_traffic.json"):
@@ -443,8 +446,10 @@ def main():
     import mi_hip_attn as mh
     lib = mh.lib()
     lib.init(0)
-    if args.deterministic:
-        lib.check(lib.mi_hip_set_deterministic(1))
+    if args.nondeterministic:
+        lib.check(lib.mi_hip_set_deterministic(0))
+    if args.prefill_f32:
+        lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream().cuda_stream
     only = set(filter(None, args.only.split(",")))
@@ -471,6 +476,10 @@ def main():
         res["prefill1024"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
         res["prefill4096"] = bench_prefill(torch, mh, lib, stream, max(10, args.steps // 10),
                                            max(2, args.warmup // 10), 4096)
+        if not args.prefill_f32:  # the float-product kernel beside the default
+            lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
+            res["prefill1024_f32"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
+            lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_SPLIT_BF16))
         print(f"# prefill 1024: {res['prefill1024']['tflops']:.2f} TF/s, 4096: "
               f"{res['prefill4096']['tflops']:.2f} TF/s", file=sys.stderr, flush=True)
     if want("d7b"):
@@ -578,6 +587,8 @@ def main():
         p1, p4 = res["prefill1024"], res["prefill4096"]
         out["prefill"] = {
             "metric": "prefill-1024 causal attn TFLOP/s (14 Q / 2 KV heads, head_dim 64, F32)",
+            "products": "f32 (v_mfma_f32_32x32x2f32)" if args.prefill_f32 else
+                        "split bf16 pairs (three v_mfma_f32_32x32x16_bf16 per product, ~1e-5 relative)",
             "tflops_1024": round(p1["tflops"], 2), "us_1024": round(p1["kernel_ms"] * 1e3, 2),
             "tflops_4096": round(p4["tflops"], 2), "us_4096": round(p4["kernel_ms"] * 1e3, 2),
             "roofline": {"bound": "mfma", "achieved": round(p1["tflops"], 2),
@@ -585,6 +596,11 @@ def main():
                          "frac": round(p1["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
                          "flops_per_launch": p1["flops"], "mfma_counters": measured_mfma()},
         }
+        if "prefill1024_f32" in res:
+            pf = res["prefill1024_f32"]
+            out["prefill"]["f32_products_1024"] = {
+                "tflops": round(pf["tflops"], 2), "us": round(pf["kernel_ms"] * 1e3, 2),
+                "frac": round(pf["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4)}
     if "sweep" in res:
         out["decode_sweep"] = {
             "workload": "24 independent layer caches, 1 query token, 14 Q / 2 KV heads, head_dim 64, "
