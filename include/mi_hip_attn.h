@@ -157,6 +157,26 @@ int mi_hip_set_deterministic(int32_t on);
 #define MI_HIP_PREFILL_SPLIT_BF16 1
 int mi_hip_set_prefill_mode(int32_t mode);
 
+/* Products of the decode kernel (one query row per head).
+ *   MI_HIP_DECODE_MATRIX: QK and PV on the matrix cores (16x16 MFMAs; head
+ *     columns padded to 16). F32 cache operands are split into bf16 pairs as
+ *     in MI_HIP_PREFILL_SPLIT_BF16 (lo.hi + hi.lo + hi.hi); an F16 cache is
+ *     used as it is, with Q and the probabilities split into f16 pairs (a
+ *     head whose |q| exceeds 2^14 is scaled by a power of two first). ~1e-5
+ *     relative per product.
+ *   MI_HIP_DECODE_VALU: float multiply-adds on the vector units (exact
+ *     float products).
+ *   MI_HIP_DECODE_AUTO (the default): per launch, the matrix cores with an
+ *     F16 cache and for F32 launches whose waves stream at least 4 sub-tiles
+ *     of 16 positions each; the vector units otherwise (there the split
+ *     operands' latency costs more than the products save).
+ * All are within the 1e-4 bar of the reference ops. Process-wide. No
+ * counterpart in the reference. */
+#define MI_HIP_DECODE_VALU 0
+#define MI_HIP_DECODE_MATRIX 1
+#define MI_HIP_DECODE_AUTO 2
+int mi_hip_set_decode_mode(int32_t mode);
+
 /* ---- device-resident KV cache ------------------------------------------ */
 
 typedef struct mi_hip_kv mi_hip_kv;

@@ -58,9 +58,21 @@
 //     merges. So a group whose parts cannot all be resident at once (other
 //     work holds the CUs) costs time, never correctness, and the fallback is
 //     counted in the workspace's status words;
-//   - teams (larger groups): every workgroup stores its record, waits for the
-//     stores and bumps its team's arrival counter; the last arriver of a team
-//     merges the team's records, and the last team merges the team results.
+//   - flat (larger groups whose launch fits the device at once): every part
+//     counts itself as started, stores its record as stamped words and then
+//     merges its own slice of the output (a range of (head, 4 dims) pairs)
+//     over every part's record: R lanes (R the power of two >= kpg) poll one
+//     pair's R records, a butterfly combines them in a fixed order, and one
+//     lane writes the 4 outputs. One poll round after the last part's stores
+//     instead of two arrival round trips and two record reads. Bounded like
+//     the early merge: a part that runs out of polls marks the start counter;
+//     if some part had not started by then it leaves its slice to the last
+//     part to start (which sees the mark in its start count and merges every
+//     slice), otherwise it keeps waiting;
+//   - teams (larger groups otherwise): every workgroup stores its record, waits
+//     for the stores and bumps its team's arrival counter; the last arriver of
+//     a team merges the team's records, and the last team merges the team
+//     results.
 // Counters come in two sets: launch e uses set e & 1, which launch e - 1
 // cleared, and clears set (e + 1) & 1 for launch e + 1, so no counter is ever
 // re-armed by a merger that might run before a late increment.
@@ -182,6 +194,53 @@ __device__ __forceinline__ void qk4(float (&s)[HS][4 / HS], const float (&q)[HS]
 
 
 
+// ---------------------------------------------------------------------------
+// Matrix-core compute (the MF kernels). Per 16-position sub-tile a wave
+// computes S^T (16 positions x 16 head columns) = K Q^T with 16x16x32 MFMAs
+// and O^T (dims x 16 head columns) += V^T P with 16x16x16 MFMAs; lane l holds
+// S^T[4 (l/16) + r][l % 16] (r < 4), which is exactly its B operand of the PV
+// product, so the probabilities never leave the lane. With an F32 cache every
+// F32 operand x is split as x = hi + lo (bf16, round to nearest) and a
+// product a b is formed as ah bh + ah bl + al bh (the lo lo term is below
+// 2^-16 of it); with an F16 cache the cache operands are exact in f16 and the
+// F32 ones (Q, P) are split as f16 pairs. Products of bf16 or f16 numbers are
+// exact in the FP32 accumulators.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+template <int N, typename V>
+__device__ __forceinline__ void split_to(const float* x, V& hi, V& lo) {
+  typedef decltype(hi[0] + hi[0]) E;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const E h = (E)x[i];
+    hi[i] = h;
+    lo[i] = (E)(x[i] - (float)h);
+  }
+}
+__device__ __forceinline__ f32x4 mfma_k32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_k32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_k16(bf16x4 a, bf16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                   0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_k16(half4_t a, half4_t b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+// V rows of the MF kernels: 16-byte slot j of row r is stored at slot
+// j ^ swv(r), so the four row groups (r / 4) of one PV operand read (16
+// consecutive elements of rows 4 g + i) fall in distinct banks.
+template <int ELT>
+__host__ __device__ constexpr int swv(int r) {
+  return ((r >> 2) & 3) * ELT;
+}
+
 template <int D, typename KT, int HS, int NWV, bool DYN>
 struct DecodeCfg {
   static constexpr int ELT = (int)sizeof(KT);
@@ -236,7 +295,7 @@ struct DecodeCfg {
 // One workgroup per CU at most is assumed only by the early protocol's
 // bounded wait (it stays correct without it); the F16 head_dim-128 variant
 // (64 KB ring) can share a CU. NWV / 4 waves per SIMD.
-template <int D, typename KT, int HS, int NWV, bool DYN>
+template <int D, typename KT, int HS, int NWV, bool DYN, bool MF>
 __global__ __launch_bounds__(NWV* kWave) __attribute__((amdgpu_waves_per_eu(NWV / 4, NWV / 4)))
 void decode_kernel(const DecodeParams p) {
   // Every scalar parameter and this grid row's item in one round of scalar
@@ -309,17 +368,18 @@ void decode_kernel(const DecodeParams p) {
   const int gid = ii * a_gpi + gl;
   unsigned* const gcnt = cset + (size_t)gid * kCtrInts;
   const bool early = a_early && kpg > 1 && kpg <= kDecodeEarlyMax;
+  const bool flat = a_early && kpg > kDecodeEarlyMax && kpg <= NWV * kWave;
   // Early protocol: count this part as started; the previous count (and the
   // merger's give-up mark, if it came first) is read at the end.
   unsigned started = 0u;
-  if (early && threadIdx.x == 0)
+  if ((early || flat) && threadIdx.x == 0)
     started = __hip_atomic_fetch_add(gcnt + kCtrStarted, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // This lane's query elements for the DPP broadcast: qv[h][e][c] =
   // Q[head0 + hb + 4h][64e + 4col + c] (head slots past G repeat head G-1 and
   // are never written out). Requested before the first cache tile.
   float qv[HS][NE][4];
-  {
+  if constexpr (!MF) {
     const char* q0 = reinterpret_cast<const char*>(it_q) + (int64_t)head0 * q_s1;
 #pragma unroll
     for (int h = 0; h < HS; ++h)
@@ -328,6 +388,29 @@ void decode_kernel(const DecodeParams p) {
         const int hs = min(hb + 4 * h, G - 1);
         const f32x4 q4 = gload<f32x4>(q0 + (int64_t)hs * q_s1 + 4 * (64 * e + 4 * col));
         qv[h][e][0] = q4.x; qv[h][e][1] = q4.y; qv[h][e][2] = q4.z; qv[h][e][3] = q4.w;
+      }
+  }
+  // MF: this lane's B operand of QK, Q[head hq][8 qg + 32 kk + i] (i < 8), as
+  // hi/lo pairs; zero for head columns past G. With an F16 cache a head whose
+  // largest |q| exceeds 2^14 is scaled by a power of two into the f16 range
+  // (undone on its scores).
+  constexpr int KK = D / 32, NT = D / 16;
+  typedef typename std::conditional<F16, f16x8, bf16x8>::type op8_t;
+  typedef typename std::conditional<F16, half4_t, bf16x4>::type op4_t;
+  const int hq = lane & 15, qg = lane >> 4;
+  float qf[KK][8];
+  op8_t qh[KK], ql[KK];
+  float sc_mf = a_scale_log2e;
+  if constexpr (MF) {
+    const char* q0 = reinterpret_cast<const char*>(it_q) + (int64_t)(head0 + min(hq, G - 1)) * q_s1;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        f32x4 q4 = gload<f32x4>(q0 + 4 * (8 * qg + 32 * kk + 4 * hh));
+        if (hq >= G) q4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) qf[kk][4 * hh + c] = q4[c];
       }
   }
 
@@ -341,7 +424,8 @@ void decode_kernel(const DecodeParams p) {
     const int r = o / C::RB;
     const int j = ((o % C::RB) / 16) ^ swz<NSLOT>(r);
     offk[i] = (unsigned)(r * ks2 + 16 * j);
-    offv[i] = (unsigned)(r * vs2 + o % C::RB);
+    offv[i] = MF ? (unsigned)(r * vs2 + 16 * (((o % C::RB) / 16) ^ swv<C::ELT>(r)))
+                 : (unsigned)(r * vs2 + o % C::RB);
   }
   lds_t* const ring = lds + C::L_RING + wv * NB * C::SLOTB;
   // QK: logical slot j of this lane's row `col`.
@@ -423,13 +507,42 @@ void decode_kernel(const DecodeParams p) {
   static_for<0, NB>([&](auto slc) { refill(slc, true); });
   // The queries were requested first; they are in registers once at most the
   // ring's loads are outstanding (the empty asm makes the compiler wait here).
+  if constexpr (!MF) {
 #pragma unroll
-  for (int h = 0; h < HS; ++h)
+    for (int h = 0; h < HS; ++h)
 #pragma unroll
-    for (int e = 0; e < NE; ++e)
-      asm volatile("" : "+v"(qv[h][e][0]), "+v"(qv[h][e][1]), "+v"(qv[h][e][2]), "+v"(qv[h][e][3]));
+      for (int e = 0; e < NE; ++e)
+        asm volatile("" : "+v"(qv[h][e][0]), "+v"(qv[h][e][1]), "+v"(qv[h][e][2]), "+v"(qv[h][e][3]));
+  } else {
+    if constexpr (F16) {
+      float amax = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qf[kk][i]));
+      amax = fmaxf(amax, __shfl_xor(amax, 16));
+      amax = fmaxf(amax, __shfl_xor(amax, 32));
+      if (amax > 16384.f) {  // 2^-e with 2^e >= amax / 2^14: exact scaling
+        const int e = ilogbf(amax) - 13;
+        const float f = ldexpf(1.f, -e);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) qf[kk][i] *= f;
+        sc_mf = a_scale_log2e * ldexpf(1.f, e);
+      }
+    }
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) split_to<8>(qf[kk], qh[kk], ql[kk]);
+  }
 
   float m[HS], l[HS], acc[HS][NE][4];
+  // MF: running max and this lane's partial sum for head column hq, and
+  // O^T[16 nt + 4 qg + r][hq] in o[nt][r].
+  float mf = -INFINITY, lf = 0.f;
+  f32x4 o[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int h = 0; h < HS; ++h) {
     m[h] = -INFINITY;
@@ -440,9 +553,118 @@ void decode_kernel(const DecodeParams p) {
       for (int jj = 0; jj < 4; ++jj) acc[h][e][jj] = 0.f;
   }
 
+  // MF: the sub-tile in ring slot SL on the matrix cores.
+  auto process_mf = [&](auto slc) __attribute__((always_inline)) {
+    constexpr int SL = decltype(slc)::value;
+    const int row0 = rows[SL];
+    constexpr int SOFF = SL * C::SLOTB;
+    wait_vmem<C::WAIT_K>();
+    // S^T = K Q^T: lane l's A operand is row hq of the sub-tile, elements
+    // 8 qg + 32 kk + i. One accumulator per product term (independent MFMA
+    // chains), summed in a fixed order.
+    const lds_t* const krow = ring + SOFF + hq * C::RB;
+    f32x4 s1 = {0.f, 0.f, 0.f, 0.f}, s2 = s1, s3 = s1;
+    if constexpr (F16) {
+      f16x8 kh[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) kh[kk] = lds_load<f16x8>(krow + 16 * ((qg + 4 * kk) ^ swz<NSLOT>(hq)));
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        s1 = mfma_k32(kh[kk], qh[kk], s1);
+        s2 = mfma_k32(kh[kk], ql[kk], s2);
+      }
+    } else {
+      bf16x8 kh[KK], kl[KK];
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const int c0 = 2 * qg + 8 * kk;
+        const f32x4 a0 = lds_load<f32x4>(krow + 16 * (c0 ^ swz<NSLOT>(hq)));
+        const f32x4 a1 = lds_load<f32x4>(krow + 16 * ((c0 + 1) ^ swz<NSLOT>(hq)));
+        const float kf[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        split_to<8>(kf, kh[kk], kl[kk]);
+      }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        s1 = mfma_k32(kh[kk], qh[kk], s1);
+        s2 = mfma_k32(kh[kk], ql[kk], s2);
+        s3 = mfma_k32(kl[kk], qh[kk], s3);
+      }
+    }
+
+    // V^T operands (column 16 nt + hq of rows 4 qg + i for N-tile nt), read
+    // while the QK products are in flight.
+    wait_vmem<C::WAIT_V>();
+    const lds_t* const vb = ring + SOFF + C::SUBB;
+    half4_t va[NT];
+    bf16x4 vh[NT], vl[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      if constexpr (F16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 4 * qg + i, el = 16 * nt + hq;
+          va[nt][i] = lds_load<_Float16>(vb + rr * C::RB + 16 * ((el / 8) ^ swv<2>(rr)) + 2 * (el % 8));
+        }
+      } else {
+        float vf[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rr = 4 * qg + i, el = 16 * nt + hq;
+          vf[i] = lds_load<float>(vb + rr * C::RB + 16 * ((el / 4) ^ swv<4>(rr)) + 4 * (el % 4));
+        }
+        split_to<4>(vf, vh[nt], vl[nt]);
+      }
+    }
+
+    // Online softmax (base 2) of head column hq over positions 4 qg + r.
+    const f32x4 sacc = F16 ? s1 + s2 : (s1 + s2) + s3;
+    float x[4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = row0 + 4 * qg + r < n_kv ? sacc[r] * sc_mf : -INFINITY;
+      mx = fmaxf(mx, x[r]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(mf, mx);
+    const float alpha = fast_exp2(mf - mn);
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(x[r] - mn);
+    lf = lf * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    mf = mn;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0ull) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] *= alpha;
+    }
+    op4_t ph, pl;
+    split_to<4>(pr, ph, pl);
+
+    // O^T += V^T P.
+    if constexpr (F16) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] = mfma_k16(va[nt], ph, o[nt]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] = mfma_k16(va[nt], pl, o[nt]);
+    } else {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] = mfma_k16(vh[nt], ph, o[nt]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] = mfma_k16(vh[nt], pl, o[nt]);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) o[nt] = mfma_k16(vl[nt], ph, o[nt]);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // slot reads done before it is refilled
+  };
+
   // The sub-tile in ring slot SL.
   auto process = [&](auto slc) __attribute__((always_inline)) {
     constexpr int SL = decltype(slc)::value;
+    if constexpr (MF) {
+      process_mf(slc);
+      return;
+    }
     const int row0 = rows[SL];
     constexpr int SOFF = SL * C::SLOTB;
     wait_vmem<C::WAIT_K>();
@@ -550,9 +772,21 @@ void decode_kernel(const DecodeParams p) {
   wait_vmem<0>();
   unsigned* const flag = reinterpret_cast<unsigned*>(lds_dyn + C::L_FLAG);
   auto dep_at = [&](int w) { return reinterpret_cast<float*>(lds_dyn + C::L_RING + w * NB * C::SLOTB); };
+  if constexpr (MF) {
+    lf += __shfl_xor(lf, 16);
+    lf += __shfl_xor(lf, 32);
+    float* dw = dep_at(wv);
+    if (hq < HSL) {
 #pragma unroll
-  for (int h = 0; h < HS; ++h) l[h] = row_sum16(l[h]);
-  {
+      for (int nt = 0; nt < NT; ++nt) *reinterpret_cast<f32x4*>(dw + hq * D + 16 * nt + 4 * qg) = o[nt];
+      if (qg == 0) {
+        dw[HSL * D + 2 * hq] = mf;
+        dw[HSL * D + 2 * hq + 1] = lf;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < HS; ++h) l[h] = row_sum16(l[h]);
     float* dw = dep_at(wv);
 #pragma unroll
     for (int h = 0; h < HS; ++h) {
@@ -691,6 +925,134 @@ void decode_kernel(const DecodeParams p) {
     wg_barrier();
     return (unsigned)__builtin_amdgcn_readfirstlane((int)flag[1]);
   };
+  // Combines (mo, lo, ao) into (m, l, a) with the stable rescaling.
+  auto fold = [](float& m, float& l, f32x4& a, float mo, float lo, f32x4 ao) __attribute__((always_inline)) {
+    const float mn = fmaxf(m, mo);
+    const float wo = m == -INFINITY ? 0.f : fast_exp2(m - mn);
+    const float wn = mo == -INFINITY ? 0.f : fast_exp2(mo - mn);
+    l = l * wo + lo * wn;
+    a = a * wo + ao * wn;
+    m = mn;
+  };
+
+  // Flat protocol layout of the group's record area (64-bit (value, epoch)
+  // words, kpg G (D + 2) of them): the npr = G D/4 pairs (pair = hs D/4 + cq)
+  // form slices of FP pairs (FP the power of two >= npr / kpg, at most D/4, so
+  // the slices tile the pairs exactly); acc value k of pair p of slice j from
+  // part q at word ((4 j + k) kpg + q) FP + p, then m and l of head slot hs
+  // from part q at 4 npr kpg + 2 (hs kpg + q) + {0, 1}. A part reading its
+  // slice reads contiguous words.
+  const int npr = G * (D / 4);
+  int FP = 1;
+  while (FP * kpg < npr) FP <<= 1;
+  auto flat_word = [&](int idx) __attribute__((always_inline)) {
+    return reinterpret_cast<unsigned long long*>(a_rec) + (int64_t)(wg - part) * (C::REC / 2) + idx;
+  };
+  auto store_flat = [&](int hs, int cq, float mx, float lt, f32x4 at) __attribute__((always_inline)) {
+    auto pk = [&](float v) { return ep | __builtin_bit_cast(unsigned, v); };
+    const int pi = hs * (D / 4) + cq, j = pi / FP, pp = pi % FP;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      __hip_atomic_store(flat_word(((4 * j + k) * kpg + part) * FP + pp), pk(at[k]), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (cq == 0) {
+      const int w = 4 * npr * kpg + 2 * (hs * kpg + part);
+      __hip_atomic_store(flat_word(w), pk(mx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(flat_word(w + 1), pk(lt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  };
+
+  // Flat merge of slice j (pairs [j FP, (j + 1) FP)) over all kpg records, at
+  // most `polls` poll rounds. In a round of PR pairs, lane t holds record
+  // t / PR of pair t % PR (consecutive lanes read consecutive words); a
+  // butterfly over the lanes of one pair combines a wave's records, and when a
+  // pair's records span several waves their results meet in LDS, combined in
+  // wave order. Every order is fixed, so the result does not depend on timing.
+  // On success the slice's outputs are written and true returned; a failed
+  // round writes none of its pairs.
+  auto merge_flat = [&](int j, int polls) __attribute__((always_inline)) -> bool {
+    constexpr int T = NWV * kWave;
+    int R = 1;
+    while (R < kpg) R <<= 1;
+    const int PR = FP < T / R ? FP : T / R;   // pairs per round
+    const int span = R * PR;                  // lanes of a round
+    const int nw = span > kWave ? span / kWave : 1;  // waves a pair's records span
+    const int t = (int)threadIdx.x;
+    const int r = t / PR;
+    for (int p0 = 0; p0 < FP; p0 += PR) {
+      const int pp = p0 + t % PR, pi = j * FP + pp;
+      const int hs = pi / (D / 4), cq = pi % (D / 4);
+      const bool act = t < span && r < kpg;
+      const int wml = 4 * npr * kpg + 2 * (hs * kpg + r);
+      auto word = [&](int k) __attribute__((always_inline)) {
+        return flat_word(k < 4 ? ((4 * j + k) * kpg + r) * FP + pp : wml + (k - 4));
+      };
+      unsigned long long w[6];
+      bool fresh = true;
+      if (act) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) w[k] = __hip_atomic_load(word(k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int n = 0;; ++n) {
+          fresh = true;
+#pragma unroll
+          for (int k = 0; k < 6; ++k) fresh &= (w[k] & kHi) == ep;
+          if (fresh || n >= polls) break;
+#pragma unroll
+          for (int k = 0; k < 6; ++k)
+            if ((w[k] & kHi) != ep) w[k] = __hip_atomic_load(word(k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      flag[2] = 1u;
+      wg_barrier();
+      if (!fresh) flag[2] = 0u;
+      wg_barrier();
+      if (flag[2] == 0u) return false;
+      float m = -INFINITY, l = 0.f;
+      f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      if (act) {
+        a = f32x4{__builtin_bit_cast(float, (unsigned)w[0]), __builtin_bit_cast(float, (unsigned)w[1]),
+                  __builtin_bit_cast(float, (unsigned)w[2]), __builtin_bit_cast(float, (unsigned)w[3])};
+        m = __builtin_bit_cast(float, (unsigned)w[4]);
+        l = __builtin_bit_cast(float, (unsigned)w[5]);
+      }
+      for (int x = PR; x < kWave && x < span; x <<= 1) {
+        const float mo = __shfl_xor(m, x), lo = __shfl_xor(l, x);
+        const f32x4 ao = {__shfl_xor(a[0], x), __shfl_xor(a[1], x), __shfl_xor(a[2], x), __shfl_xor(a[3], x)};
+        fold(m, l, a, mo, lo, ao);
+      }
+      if (nw > 1) {
+        float* tmp = reinterpret_cast<float*>(lds_dyn + C::L_TMP);
+        const int wi = t / kWave;
+        if (wi < nw && (t & (kWave - 1)) < PR) {
+          float* e = tmp + ((t % PR) * nw + wi) * 6;
+          e[0] = m; e[1] = l; e[2] = a[0]; e[3] = a[1]; e[4] = a[2]; e[5] = a[3];
+        }
+        wg_barrier();
+        if (t < PR)
+          for (int q = 1; q < nw; ++q) {
+            const float* e = tmp + (t * nw + q) * 6;
+            fold(m, l, a, e[0], e[1], f32x4{e[2], e[3], e[4], e[5]});
+          }
+        wg_barrier();
+      }
+      if (t < PR) {
+        float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
+        gstore<f32x4>(o + 4 * cq, a * (1.f / l));
+      }
+    }
+    return true;
+  };
+  // NaN outputs for slices [ja, jb) of a group whose records never arrived.
+  auto lost_slices = [&](int ja, int jb) __attribute__((always_inline)) {
+    for (int pi = ja * FP + (int)threadIdx.x; pi < jb * FP; pi += NWV * kWave) {
+      const int hs = pi / (D / 4), cq = pi % (D / 4);
+      float* o = reinterpret_cast<float*>(reinterpret_cast<char*>(it_out) + (int64_t)(head0 + hs) * o_s1);
+      gstore<f32x4>(o + 4 * cq, f32x4{NAN, NAN, NAN, NAN});
+    }
+    if (threadIdx.x == 0) __hip_atomic_fetch_add(a_status + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  constexpr unsigned kGaveUp = 1u << 16;
+  constexpr int kLongWait = 1 << 20;  // rounds; only a broken invariant exhausts it
 
   {
     // wave wv combines head slots wv + NWV t; lane = (slot t, float4 cq)
@@ -723,6 +1085,8 @@ void decode_kernel(const DecodeParams p) {
         e[1] = lt;
         *reinterpret_cast<f32x2*>(e + 2) = f32x2{at[0], at[1]};
         *reinterpret_cast<f32x2*>(e + 4) = f32x2{at[2], at[3]};
+      } else if (flat) {
+        if (hs < G) store_flat(hs, cq, mx, lt, at);
       } else if (early) {
         store_stamped(hs, cq, mx, lt, at);
       } else {
@@ -736,9 +1100,31 @@ void decode_kernel(const DecodeParams p) {
     }
   }
   if (kpg == 1) return;
+  if (flat) {
+    // Part j < npr / FP merges slice j.
+    const int n_slices = npr / FP;
+    const bool mine = part < n_slices;
+    if (threadIdx.x == 0) flag[3] = started;
+    wg_barrier();
+    const unsigned st = (unsigned)__builtin_amdgcn_readfirstlane((int)flag[3]);
+    if (mine && !merge_flat(part, a_max_polls)) {
+      // Out of polls: mark the start counter. If some part had not started,
+      // leave this slice to the last part to start; otherwise every part is
+      // running or done, and the records arrive.
+      const unsigned g0 = atomic_bcast(gcnt + kCtrStarted, kGaveUp);
+      if ((int)(g0 & (kGaveUp - 1)) < kpg) {
+        if (threadIdx.x == 0) __hip_atomic_fetch_add(a_status + 0, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+      }
+      if (!merge_flat(part, kLongWait)) lost_slices(part, part + 1);
+    }
+    // The last part to start, after some part gave up: every slice.
+    if ((int)(st & (kGaveUp - 1)) == kpg - 1 && st >= kGaveUp)
+      for (int j = 0; j < n_slices; ++j)
+        if (!merge_flat(j, kLongWait)) lost_slices(j, j + 1);
+    return;
+  }
   if (early) {
-    constexpr unsigned kGaveUp = 1u << 16;
-    constexpr int kLongWait = 1 << 20;  // rounds; only a broken invariant exhausts it
     int own_part = part;
     if (!merger) {
       // The record is stored. Parts that started before any give-up mark
@@ -917,27 +1303,34 @@ constexpr int decode_waves() {
   return D == 64 ? 8 : 4;
 }
 
-template <int D, typename KT, int HS, bool DYN>
+template <int D, typename KT, int HS, bool DYN, bool MF>
 static hipError_t launch_decode_t(const DecodeParams& p, int grid_x, int n_items, hipStream_t stream) {
   constexpr int NWV = decode_waves<D, KT>();
   typedef DecodeCfg<D, KT, HS, NWV, DYN> C;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, KT, HS, NWV, DYN>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&decode_kernel<D, KT, HS, NWV, DYN, MF>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, C::L_TOTAL);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV, DYN>), dim3((unsigned)grid_x, (unsigned)n_items), dim3(NWV * kWave),
-                     C::L_TOTAL, stream, p);
+  hipLaunchKernelGGL((decode_kernel<D, KT, HS, NWV, DYN, MF>), dim3((unsigned)grid_x, (unsigned)n_items),
+                     dim3(NWV * kWave), C::L_TOTAL, stream, p);
   return hipGetLastError();
 }
 
-template <int D, typename KT>
-static hipError_t launch_decode_h(const DecodeParams& p, int grid_x, int n_items, int group, bool dyn,
+template <int D, typename KT, bool MF>
+static hipError_t launch_decode_m(const DecodeParams& p, int grid_x, int n_items, int group, bool dyn,
                                   hipStream_t stream) {
   if (group > 4)
-    return dyn ? launch_decode_t<D, KT, 2, true>(p, grid_x, n_items, stream)
-               : launch_decode_t<D, KT, 2, false>(p, grid_x, n_items, stream);
-  return dyn ? launch_decode_t<D, KT, 1, true>(p, grid_x, n_items, stream)
-             : launch_decode_t<D, KT, 1, false>(p, grid_x, n_items, stream);
+    return dyn ? launch_decode_t<D, KT, 2, true, MF>(p, grid_x, n_items, stream)
+               : launch_decode_t<D, KT, 2, false, MF>(p, grid_x, n_items, stream);
+  return dyn ? launch_decode_t<D, KT, 1, true, MF>(p, grid_x, n_items, stream)
+             : launch_decode_t<D, KT, 1, false, MF>(p, grid_x, n_items, stream);
+}
+
+template <int D, typename KT>
+static hipError_t launch_decode_h(const DecodeParams& p, int grid_x, int n_items, int group, bool dyn, bool mf,
+                                  hipStream_t stream) {
+  return mf ? launch_decode_m<D, KT, true>(p, grid_x, n_items, group, dyn, stream)
+            : launch_decode_m<D, KT, false>(p, grid_x, n_items, group, dyn, stream);
 }
 
 int decode_wg_waves(int head_dim, bool f16) {
@@ -972,14 +1365,14 @@ size_t decode_record_floats(int head_dim, int group) {
 }
 
 hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,
-                         bool dyn, hipStream_t stream) {
+                         bool dyn, bool mf, hipStream_t stream) {
   if (grid_x < 1 || n_items < 1 || n_items > kDecodeMaxItems) return hipErrorInvalidValue;
   if (head_dim == 64)
-    return f16 ? launch_decode_h<64, _Float16>(p, grid_x, n_items, group, dyn, stream)
-               : launch_decode_h<64, float>(p, grid_x, n_items, group, dyn, stream);
+    return f16 ? launch_decode_h<64, _Float16>(p, grid_x, n_items, group, dyn, mf, stream)
+               : launch_decode_h<64, float>(p, grid_x, n_items, group, dyn, mf, stream);
   if (head_dim == 128)
-    return f16 ? launch_decode_h<128, _Float16>(p, grid_x, n_items, group, dyn, stream)
-               : launch_decode_h<128, float>(p, grid_x, n_items, group, dyn, stream);
+    return f16 ? launch_decode_h<128, _Float16>(p, grid_x, n_items, group, dyn, mf, stream)
+               : launch_decode_h<128, float>(p, grid_x, n_items, group, dyn, mf, stream);
   return hipErrorInvalidValue;
 }
 

@@ -23,7 +23,7 @@ int decode_team(int head_dim, bool f16, int group);     // workgroups per combin
 // Grid (grid_x, n_items): row y serves p.item[y]; workgroups past an item's
 // gpi * kpg leave at once.
 hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,
-                         bool dyn, hipStream_t stream);
+                         bool dyn, bool mf, hipStream_t stream);
 // n words at p set to v on `stream` (a kernel, so it may sit in a graph).
 hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t stream);
 

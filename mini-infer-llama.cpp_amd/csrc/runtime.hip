@@ -78,6 +78,7 @@ struct State {
   Knobs knobs;
   std::atomic<int> deterministic{1};  // fixed per-wave takes in the fused kernels
   std::atomic<int> prefill_mode{MI_HIP_PREFILL_SPLIT_BF16};  // matrix cores of the prefill kernel
+  std::atomic<int> decode_mode{MI_HIP_DECODE_AUTO};          // matrix cores of the decode kernel
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
   mi_hip_workspace* scratch_ws = nullptr;  // over the static scratch array (never freed)
 };
@@ -137,6 +138,7 @@ struct DecodePlan {
   int n_wg = 0;    // workgroups with work (records)
   int grid_x = 0;  // the widest item's workgroups (grid rows are items)
   bool dyn = false;     // dynamic sub-tile claims
+  bool long_waves = false;  // every wave streams 4 or more sub-tiles on average
 };
 
 DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim,
@@ -167,6 +169,7 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   }
   for (int i = 0; i < n_items; ++i) p.grid_x = std::max(p.grid_x, gpi * it[i].kpg);
   p.n_wg = (int)wg;
+  p.long_waves = sub >= 4 * wg * waves;
   return p;
 }
 
@@ -484,7 +487,9 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
     // (knob 2 forces it: tests of the fallback for parts that start late).
     p.early = g.knobs.early == 2 || (plan.n_wg <= g.n_cu && g.knobs.early != 0);
     if ((rc = ws_next_epoch(ws, cnt * gpi, stream, &p.epoch, &p.clear_groups))) return rc;
-    hipError_t e = mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, stream);
+    const int dmode = g.decode_mode.load();
+    const bool mf = dmode == MI_HIP_DECODE_MATRIX || (dmode == MI_HIP_DECODE_AUTO && (r0.f16 || plan.long_waves));
+    hipError_t e = mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, mf, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     base += cnt;
   }
@@ -920,6 +925,13 @@ int mi_hip_set_prefill_mode(int32_t mode) {
   if (mode != MI_HIP_PREFILL_F32 && mode != MI_HIP_PREFILL_SPLIT_BF16)
     return fail(MI_HIP_E_INVALID, "prefill mode %d: MI_HIP_PREFILL_F32 (0) or MI_HIP_PREFILL_SPLIT_BF16 (1)", mode);
   g.prefill_mode.store(mode);
+  return MI_HIP_OK;
+}
+
+int mi_hip_set_decode_mode(int32_t mode) {
+  if (mode != MI_HIP_DECODE_VALU && mode != MI_HIP_DECODE_MATRIX && mode != MI_HIP_DECODE_AUTO)
+    return fail(MI_HIP_E_INVALID, "decode mode %d: MI_HIP_DECODE_VALU (0), _MATRIX (1) or _AUTO (2)", mode);
+  g.decode_mode.store(mode);
   return MI_HIP_OK;
 }
 

@@ -30,6 +30,9 @@ MI_TENSOR_FLAG_KV = 1 << 3
 
 MI_HIP_PREFILL_F32 = 0
 MI_HIP_PREFILL_SPLIT_BF16 = 1
+MI_HIP_DECODE_VALU = 0
+MI_HIP_DECODE_MATRIX = 1
+MI_HIP_DECODE_AUTO = 2
 
 MI_HIP_QWEN2_ATTN_FUSED = 0
 MI_HIP_QWEN2_ATTN_REFERENCE_ORDER = 1
@@ -172,6 +175,7 @@ SIGNATURES = {
     "mi_hip_workspace_set_poll_limit": ([_P, ctypes.c_int32], _I),
     "mi_hip_set_deterministic": ([ctypes.c_int32], _I),
     "mi_hip_set_prefill_mode": ([ctypes.c_int32], _I),
+    "mi_hip_set_decode_mode": ([ctypes.c_int32], _I),
     "mi_hip_decode_tuning": ([ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32], _I),
     "mi_hip_kv_view": ([_P, _I, _I, ctypes.POINTER(ctypes.c_void_p),
                         ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_size_t)], _I),

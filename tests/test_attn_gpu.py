@@ -33,8 +33,9 @@ def dev(a, dtype=None):
     return t.cuda()
 
 
-def fused(hip, stream, q, k, v, n_past, scale, f16=False):
-    """Runs mi_hip_attn_fwd on explicit device tensors; returns host output."""
+def fused(hip, stream, q, k, v, n_past, scale, f16=False, ws=None):
+    """Runs mi_hip_attn_fwd on explicit device tensors (with the decode
+    workspace `ws`, else the library's); returns host output."""
     import torch
     assert k.shape == v.shape and k.shape[2] == q.shape[2] and q.shape[1] % k.shape[1] == 0
     assert n_past + q.shape[0] <= k.shape[0]
@@ -42,7 +43,7 @@ def fused(hip, stream, q, k, v, n_past, scale, f16=False):
     dk = dev(k.astype(np.float16)) if f16 else dev(k)
     dv = dev(v.astype(np.float16)) if f16 else dev(v)
     out = torch.full(q.shape, float("nan"), dtype=torch.float32, device="cuda")
-    a = mh.attn_args(dq, out, q.shape[1] // k.shape[1], n_past, scale, stream, k=dk, v=dv)
+    a = mh.attn_args(dq, out, q.shape[1] // k.shape[1], n_past, scale, stream, k=dk, v=dv, ws=ws)
     hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
     torch.cuda.synchronize()
     return out.cpu().numpy()
@@ -55,7 +56,7 @@ def ref_out(oracle, q, k, v, n_past, scale, f16=False, threads=16):
     return oracle.attention(q, k, v, n_past, scale, threads)[2]
 
 
-def test_golden_cases(hip, stream, golden_manifest):
+def test_golden_cases(hip, stream, golden_manifest, decode_mode):
     for name, c in golden_manifest["cases"].items():
         if c["head_dim"] not in (64, 128):
             continue  # head_dim 4 (tiny model) runs through the node operators
@@ -70,7 +71,7 @@ def test_golden_cases(hip, stream, golden_manifest):
 
 
 @pytest.mark.parametrize("n_kv", [1, 63, 64, 65, 128, 1000, 1024, 4096, 16384, 32768])
-def test_decode_sweep_qwen05_shape(hip, stream, oracle, n_kv):
+def test_decode_sweep_qwen05_shape(hip, stream, oracle, n_kv, decode_mode):
     print("decode n_kv", n_kv, flush=True)
     q, k, v = cpu_attention.make_inputs(1236 + n_kv, 64, 14, 2, n_kv, 1)
     got = fused(hip, stream, q, k, v, n_kv - 1, 0.125)
@@ -79,7 +80,7 @@ def test_decode_sweep_qwen05_shape(hip, stream, oracle, n_kv):
 
 @pytest.mark.parametrize("n_rep,hkv,d", [(1, 4, 64), (2, 2, 64), (4, 2, 128), (8, 2, 64),
                                          (3, 2, 64), (6, 1, 128), (14, 1, 64)])
-def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d):
+def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d, decode_mode):
     n_kv = 777
     q, k, v = cpu_attention.make_inputs(31 + n_rep, d, n_rep * hkv, hkv, n_kv, 1)
     scale = float(np.float32(1) / np.sqrt(np.float32(d)))
@@ -94,13 +95,38 @@ def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d):
 @pytest.mark.parametrize("n_rep,hkv,d,n_kv", [(1, 4, 64, 777), (2, 2, 128, 777), (4, 2, 128, 777),
                                               (7, 2, 64, 1), (7, 2, 64, 17), (7, 2, 64, 777),
                                               (7, 2, 64, 4096), (8, 1, 128, 2000)])
-def test_decode_f16_cache_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv):
+def test_decode_f16_cache_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv, decode_mode):
     print("f16 decode", n_rep, hkv, d, n_kv, flush=True)
     q, k, v = cpu_attention.make_inputs(900 + 7 * n_rep + d + n_kv, d, n_rep * hkv, hkv, n_kv, 1)
     scale = float(np.float32(1) / np.sqrt(np.float32(d)))
     got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=True)
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=True), TOL_F32, "widened")
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
+
+
+@pytest.fixture(params=[mh.MI_HIP_DECODE_MATRIX, mh.MI_HIP_DECODE_VALU], ids=["matrix", "valu"])
+def decode_mode(request, hip):
+    """Runs a decode test on each decode kernel (matrix cores, vector units);
+    the library default picks one of them per launch."""
+    hip.check(hip.mi_hip_set_decode_mode(request.param))
+    yield request.param
+    hip.check(hip.mi_hip_set_decode_mode(mh.MI_HIP_DECODE_AUTO))
+
+
+def test_decode_f16_cache_large_queries(hip, stream, oracle, decode_mode):
+    # Queries far outside the f16 range (|q| up to ~4e5 on some heads, others
+    # unscaled): the matrix kernel scales such a head's f16 operand by a power
+    # of two and undoes it on the scores; the result must not change.
+    n_kv, d = 1500, 128
+    q, k, v = cpu_attention.make_inputs(4242, d, 8, 2, n_kv, 1)
+    q = q.copy()
+    q[0, 1] *= 1e5
+    q[0, 6] *= 3e4
+    q[0, 7] *= 50.0
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=True)
+    assert np.isfinite(got).all()
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=True), TOL_F32, "widened")
 
 
 @pytest.fixture()
@@ -121,7 +147,7 @@ def tuning(hip):
 @pytest.mark.parametrize("kpg,early", [(2, 1), (5, 1), (8, 1), (8, 0), (9, 1), (24, 0), (40, 1), (100, 0)])
 @pytest.mark.parametrize("d,f16", [(64, False), (128, True)])
 @pytest.mark.parametrize("claim", [1, 0])
-def test_decode_forced_split(hip, stream, oracle, tuning, kpg, early, d, f16, claim):
+def test_decode_forced_split(hip, stream, oracle, tuning, kpg, early, d, f16, claim, decode_mode):
     # claim 1: sub-tiles claimed from the group counter (dynamic takes, which
     # the deterministic mode turns off); 0: every kpg-th sub-tile per part,
     # in fixed (deterministic) order
@@ -133,6 +159,55 @@ def test_decode_forced_split(hip, stream, oracle, tuning, kpg, early, d, f16, cl
     scale = float(np.float32(1) / np.sqrt(np.float32(d)))
     got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=f16)
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=f16), TOL_F32)
+
+
+# The flat merge (more than 8 parts, launch resident at once): every part
+# merges its slice of the output over all parts' records. One KV head group, so
+# that up to 256 parts fit the device: 2..64 lanes per pair (one wave) and
+# 128/256 (waves meeting in LDS).
+@pytest.mark.parametrize("d,f16,kpg", [(64, False, 9), (64, False, 33), (64, False, 100), (64, False, 256),
+                                       (128, True, 64), (128, True, 129), (128, True, 256)])
+def test_decode_flat_merge(hip, stream, oracle, tuning, d, f16, kpg, decode_mode):
+    print("flat merge", d, f16, kpg, flush=True)
+    tuning(kpg=kpg, early=1)
+    waves = 8 if d == 64 else 4
+    n_kv = 16 * waves * kpg + 37  # every wave of every part has a sub-tile, the last one partial
+    q, k, v = cpu_attention.make_inputs(8800 + kpg + d, d, 7, 1, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    ws = hip.workspace_create(1, 7, d)
+    try:
+        got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=f16, ws=ws)
+        rc, fallbacks, lost = hip.workspace_check(ws, stream)
+        assert rc == 0 and lost == 0 and fallbacks == 0
+    finally:
+        hip.check(hip.mi_hip_workspace_destroy(ws))
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=f16), TOL_F32)
+
+
+def test_flat_merge_fallback_is_exact(hip, stream, oracle, tuning):
+    # 24 items x 2 groups x 24 parts = 1152 workgroups (one per CU at a time)
+    # with the flat merge forced: a group that straddles the resident set (48
+    # workgroups per item do not divide the CU count) has parts that run out
+    # of polls (limit 0) while others have not started; they mark the start
+    # counter and leave their slices to the last part to start, which merges
+    # every slice. Groups resident as a whole keep waiting. Exact either way.
+    import torch
+    tuning(kpg=24, early=2)
+    ws = hip.workspace_create(2, 14, 64)
+    try:
+        hip.check(hip.mi_hip_workspace_set_poll_limit(ws, 0))
+        total = 0
+        for rep in range(3):
+            ins, outs, _ = batch_24(hip, stream, 4096, 9100 + 100 * rep, ws=ws)
+            torch.cuda.synchronize()
+            check_batch_24(oracle, ins, outs, 4096, f"rep {rep}")
+            rc, fallbacks, lost = hip.workspace_check(ws, stream)
+            print("1152 workgroups: fallbacks", fallbacks, "lost", lost, flush=True)
+            assert rc == 0 and lost == 0
+            total += fallbacks
+        assert total > 0
+    finally:
+        hip.check(hip.mi_hip_workspace_destroy(ws))
 
 
 @pytest.fixture()
@@ -152,7 +227,7 @@ def dynamic_takes(hip):
 
 
 @pytest.mark.parametrize("kpg", [0, 3, 8, 24])
-def test_deterministic_decode_repeats_bit_for_bit(hip, stream, oracle, tuning, deterministic, kpg):
+def test_deterministic_decode_repeats_bit_for_bit(hip, stream, oracle, tuning, deterministic, kpg, decode_mode):
     # With fixed per-wave takes every merge runs in a fixed order, so five
     # launches of one problem give the same bits (planned split and forced
     # splits over both merge protocols), and they meet the oracle's bar.
@@ -206,7 +281,7 @@ def test_decode_back_to_back_launches_share_no_records(hip, stream, oracle):
         assert_close(out.cpu().numpy(), ref_out(oracle, q, k, v, n_kv - 1, 0.125), TOL_F32, f"launch {i}")
 
 
-def test_decode_qwen7b_shape_f16_cache(hip, stream, oracle):
+def test_decode_qwen7b_shape_f16_cache(hip, stream, oracle, decode_mode):
     n_kv = 8192
     q, k, v = cpu_attention.make_inputs(1238, 128, 28, 4, n_kv, 1)
     scale = float(np.float32(1) / np.sqrt(np.float32(128)))
@@ -326,7 +401,7 @@ def test_two_workspaces_decode_concurrently(hip, oracle):
 
 @pytest.mark.parametrize("det", [1, 0])
 @pytest.mark.parametrize("early", [1, 0])
-def test_decode_batch_24_layers(hip, stream, oracle, tuning, early, det):
+def test_decode_batch_24_layers(hip, stream, oracle, tuning, early, det, decode_mode):
     # both cross-workgroup combines at the headline shape (5 workgroups per
     # group): the first finisher polling stamped records, and the counters
     import torch
