@@ -114,48 +114,73 @@ __global__ void silu_mul_q8_kernel(const float* gu, int64_t gu_ld, int F, char* 
   gstore<signed char>(blk + 4 + (e & 31), (signed char)q);
 }
 
-// mi_qwen2_sample_greedy (src/model_qwen2.cpp:690-700): the first index of
-// the maximum. Each thread scans its indices in order with a strict
-// comparison; partial results merge by value, then by the smaller index.
-constexpr int kArgmaxThreads = 1024;
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* v, int n, int32_t* out) {
-  __shared__ float sv[kArgmaxThreads / kWave];
-  __shared__ int si[kArgmaxThreads / kWave];
-  float best = -INFINITY;
-  int bi = -1;
-  for (int i = threadIdx.x; i < n; i += kArgmaxThreads) {
-    const float x = gload<float>(v + i);
-    if (bi < 0 || x > best) {
-      best = x;
-      bi = i;
-    }
-  }
-  auto better = [](float a, int ia, float b, int ib) {
-    if (ib < 0) return false;
-    if (ia < 0) return true;
-    return b > a || (b == a && ib < ia);
-  };
+// mi_qwen2_sample_greedy (src/model_qwen2.cpp:690-700): starting from index 0,
+// an index replaces the best only if its value is strictly greater. So the
+// result is the first index of the largest non-NaN value when v[0] is not NaN,
+// and 0 when it is (nothing compares greater than NaN). Two launches: each of
+// kArgmaxParts workgroups scans one contiguous chunk (float4 loads, several in
+// flight per lane) for its first largest non-NaN value; one wave merges the
+// chunk results in chunk order (larger value, then smaller index).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kArgmaxParts = 128;
+constexpr int kArgmaxThreads = 256;
+struct ArgBest {
+  float v;
+  int i;  // -1: no candidate yet
+};
+__device__ inline ArgBest arg_better(ArgBest a, ArgBest b) {
+  if (b.i < 0) return a;
+  if (a.i < 0 || b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+  return a;
+}
+__device__ inline ArgBest arg_wave(ArgBest b) {
   for (int off = kWave / 2; off > 0; off >>= 1) {
-    const float ob = __shfl_xor(best, off);
-    const int oi = __shfl_xor(bi, off);
-    if (better(best, bi, ob, oi)) {
-      best = ob;
-      bi = oi;
+    const ArgBest o{__shfl_xor(b.v, off), __shfl_xor(b.i, off)};
+    b = arg_better(b, o);
+  }
+  return b;
+}
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_part_kernel(const float* v, int n, int vec, float* pv,
+                                                                     int* pi) {
+  __shared__ ArgBest sb[kArgmaxThreads / kWave];
+  const int chunk = ((n + kArgmaxParts - 1) / kArgmaxParts + 3) & ~3;  // a multiple of 4 elements
+  const int b0 = min(n, (int)blockIdx.x * chunk), b1 = min(n, b0 + chunk);
+  ArgBest best{0.f, -1};
+  auto take = [&](float x, int i) {
+    if (!(x != x) && (best.i < 0 || x > best.v)) best = ArgBest{x, i};
+  };
+  // float4 loads when v is 16-byte aligned (chunks start at multiples of 4)
+  const int n4 = vec ? (b1 - b0) / 4 : 0;
+  for (int j0 = threadIdx.x; j0 < n4; j0 += 4 * kArgmaxThreads) {
+    f32x4 q[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u * kArgmaxThreads;
+      q[u] = j < n4 ? gload<f32x4>(v + b0 + 4 * j) : f32x4{NAN, NAN, NAN, NAN};
     }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) take(q[u][c], b0 + 4 * (j0 + u * kArgmaxThreads) + c);
   }
-  const int wv = threadIdx.x / kWave;
-  if ((threadIdx.x & (kWave - 1)) == 0) {
-    sv[wv] = best;
-    si[wv] = bi;
-  }
+  for (int i = b0 + 4 * n4 + threadIdx.x; i < b1; i += kArgmaxThreads) take(gload<float>(v + i), i);
+  best = arg_wave(best);
+  if ((threadIdx.x & (kWave - 1)) == 0) sb[threadIdx.x / kWave] = best;
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int k = 1; k < kArgmaxThreads / kWave; ++k)
-      if (better(best, bi, sv[k], si[k])) {
-        best = sv[k];
-        bi = si[k];
-      }
-    gstore<int>(out, bi < 0 ? 0 : bi);
+    for (int k = 1; k < kArgmaxThreads / kWave; ++k) best = arg_better(best, sb[k]);
+    gstore<float>(pv + blockIdx.x, best.v);
+    gstore<int>(pi + blockIdx.x, best.i);
+  }
+}
+__global__ __launch_bounds__(kWave) void argmax_final_kernel(const float* v, const float* pv, const int* pi,
+                                                               int32_t* out) {
+  ArgBest best{0.f, -1};
+  for (int k = threadIdx.x; k < kArgmaxParts; k += kWave) best = arg_better(best, ArgBest{pv[k], pi[k]});
+  best = arg_wave(best);
+  if (threadIdx.x == 0) {
+    const float v0 = gload<float>(v);
+    gstore<int>(out, (v0 != v0 || best.i < 0) ? 0 : best.i);
   }
 }
 
@@ -192,6 +217,8 @@ struct mi_hip_qwen2 {
   float *x = nullptr, *qkv = nullptr, *ao = nullptr, *gu = nullptr, *logits = nullptr;
   char* aq = nullptr;
   int32_t *ids = nullptr, *next = nullptr;
+  float* arg_v = nullptr;      // argmax: one (value, index) per chunk
+  int32_t* arg_i = nullptr;
   int32_t *h_ids = nullptr, *h_next = nullptr;  // pinned staging
   float* rope_cs = nullptr;  // (cos, sin) of every (position < n_ctx, pair), from the host's libm
   int attn_mode = MI_HIP_QWEN2_ATTN_FUSED;
@@ -390,6 +417,7 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   const size_t olog = a; a = mi::align256(a + 4 * V * T);
   const size_t oids = a; a = mi::align256(a + 4 * T);
   const size_t onext = a; a = mi::align256(a + 4);
+  const size_t oarg = a; a = mi::align256(a + 8 * mi::kArgmaxParts);
   const size_t ocs = a; a = mi::align256(a + 4 * 2 * (size_t)n_ctx * (hd / 2));
   if ((rc = mi::rt_alloc(&p, a, "qwen2 activations"))) return rc;
   m->abuf = static_cast<char*>(p);
@@ -402,6 +430,8 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   m->logits = reinterpret_cast<float*>(m->abuf + olog);
   m->ids = reinterpret_cast<int32_t*>(m->abuf + oids);
   m->next = reinterpret_cast<int32_t*>(m->abuf + onext);
+  m->arg_v = reinterpret_cast<float*>(m->abuf + oarg);
+  m->arg_i = reinterpret_cast<int32_t*>(m->abuf + oarg + 4 * mi::kArgmaxParts);
   m->rope_cs = reinterpret_cast<float*>(m->abuf + ocs);
   {
     // the engine's angles (src/ops_cpu.cpp:287-291): freq = powf(base, -(2p)/n_dims),
@@ -630,9 +660,12 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
   if ((rc = proj(m, m->lm_head, m->row_e, hp.n_vocab, E, {m->x + (int64_t)first * E, m->out_norm}, n_out,
                  m->logits, hp.n_vocab, nullptr, 0)))
     return rc;
-  hipLaunchKernelGGL(mi::argmax_kernel, dim3(1), dim3(mi::kArgmaxThreads), 0, st,
-                     m->logits + (int64_t)(n_out - 1) * hp.n_vocab, hp.n_vocab, m->next);
+  const float* last_row = m->logits + (int64_t)(n_out - 1) * hp.n_vocab;
+  hipLaunchKernelGGL(mi::argmax_part_kernel, dim3(mi::kArgmaxParts), dim3(mi::kArgmaxThreads), 0, st, last_row,
+                     hp.n_vocab, (reinterpret_cast<uintptr_t>(last_row) & 15) == 0 ? 1 : 0, m->arg_v, m->arg_i);
   Q2_TRY(hipGetLastError(), "argmax launch");
+  hipLaunchKernelGGL(mi::argmax_final_kernel, dim3(1), dim3(mi::kWave), 0, st, last_row, m->arg_v, m->arg_i, m->next);
+  Q2_TRY(hipGetLastError(), "argmax merge launch");
   Q2_TRY(hipMemcpyAsync(m->h_next, m->next, 4, hipMemcpyDeviceToHost, st), "next id copy");
   if (logits_out)
     Q2_TRY(hipMemcpyAsync(logits_out, m->logits, 4 * (size_t)hp.n_vocab * n_out, hipMemcpyDeviceToHost, st),
