@@ -445,6 +445,8 @@ void decode_kernel(const DecodeParams p) {
   const char* const kg = it_k + (int64_t)g * k_s1;
   const char* const vg = it_v + (int64_t)g * v_s1;
   int rows[NB];
+  bool drained = false;  // a refill past the share was skipped (wave-uniform)
+
   auto issue = [&](auto slc, int t) __attribute__((always_inline)) {
     constexpr int SL = decltype(slc)::value;
     lds_t* const slot = ring + SL * C::SLOTB;
@@ -501,19 +503,32 @@ void decode_kernel(const DecodeParams p) {
       pend[SL] = c;
     } else {
       t = lds_take();
+      if (drained) {  // nothing more for this wave (set by the first fill)
+        rows[SL] = -1;
+        return;
+      }
     }
     issue(slc, t);
   };
-  static_for<0, NB>([&](auto slc) { refill(slc, true); });
   // The queries were requested first; they are in registers once at most the
-  // ring's loads are outstanding (the empty asm makes the compiler wait here).
+  // ring's loads are outstanding (the empty asm makes the compiler wait here:
+  // its wait counts the loads issued since, so every path below issues a
+  // number of them known at compile time).
+  auto q_ready = [&]() __attribute__((always_inline)) {
   if constexpr (!MF) {
 #pragma unroll
     for (int h = 0; h < HS; ++h)
 #pragma unroll
       for (int e = 0; e < NE; ++e)
-        asm volatile("" : "+v"(qv[h][e][0]), "+v"(qv[h][e][1]), "+v"(qv[h][e][2]), "+v"(qv[h][e][3]));
+        asm volatile("" : "+v"(qv[h][e][0]), "+v"(qv[h][e][1]), "+v"(qv[h][e][2]), "+v"(qv[h][e][3])::"memory");
   } else {
+    // (the memory clobber keeps the compiler from hoisting the split, and
+    // with it the wait for the queries, above the ring's loads)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int i = 0; i < 8; i += 4)
+        asm volatile("" : "+v"(qf[kk][i]), "+v"(qf[kk][i + 1]), "+v"(qf[kk][i + 2]), "+v"(qf[kk][i + 3])::"memory");
     if constexpr (F16) {
       float amax = 0.f;
 #pragma unroll
@@ -534,6 +549,21 @@ void decode_kernel(const DecodeParams p) {
     }
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) split_to<8>(qf[kk], qh[kk], ql[kk]);
+  }
+  };
+  // First fill: every slot (past the share through a zero-sized resource),
+  // so that the loads after the queries' are a fixed count. In the vector
+  // kernel (the short launches' choice), a wave whose share ends within it
+  // issues no refill afterwards and from then on waits for all of its loads
+  // instead of the fixed counts, which assume one refill per slot (measured:
+  // -0.4 to -0.5 us on one-layer launches of 1 sub-tile per wave; a wave
+  // that streams keeps issuing its empty refills to the end of its loop:
+  // skipping them there, or in the matrix-core kernel, measured slower).
+  static_for<0, NB>([&](auto slc) { refill(slc, true); });
+  q_ready();
+  if constexpr (!DYN && !MF) {
+#pragma unroll
+    for (int s2 = 0; s2 < NB; ++s2) drained |= rows[s2] < 0;
   }
 
   float m[HS], l[HS], acc[HS][NE][4];
@@ -558,7 +588,10 @@ void decode_kernel(const DecodeParams p) {
     constexpr int SL = decltype(slc)::value;
     const int row0 = rows[SL];
     constexpr int SOFF = SL * C::SLOTB;
-    wait_vmem<C::WAIT_K>();
+    if (drained)
+      wait_vmem<0>();
+    else
+      wait_vmem<C::WAIT_K>();
     // S^T = K Q^T: lane l's A operand is row hq of the sub-tile, elements
     // 8 qg + 32 kk + i. One accumulator per product term (independent MFMA
     // chains), summed in a fixed order.
@@ -593,7 +626,7 @@ void decode_kernel(const DecodeParams p) {
 
     // V^T operands (column 16 nt + hq of rows 4 qg + i for N-tile nt), read
     // while the QK products are in flight.
-    wait_vmem<C::WAIT_V>();
+    if (!drained) wait_vmem<C::WAIT_V>();  // (drained: all landed above)
     const lds_t* const vb = ring + SOFF + C::SUBB;
     half4_t va[NT];
     bf16x4 vh[NT], vl[NT];
@@ -667,7 +700,10 @@ void decode_kernel(const DecodeParams p) {
     }
     const int row0 = rows[SL];
     constexpr int SOFF = SL * C::SLOTB;
-    wait_vmem<C::WAIT_K>();
+    if (drained)
+      wait_vmem<0>();
+    else
+      wait_vmem<C::WAIT_K>();
 
     // K slots are requested up to KW ahead of their multiply-adds (LDS reads
     // complete in order, so each block waits only for its own).
@@ -737,7 +773,7 @@ void decode_kernel(const DecodeParams p) {
         pv[h][4 * q4 + 0] = t.x; pv[h][4 * q4 + 1] = t.y; pv[h][4 * q4 + 2] = t.z; pv[h][4 * q4 + 3] = t.w;
       }
 
-    wait_vmem<C::WAIT_V>();
+    if (!drained) wait_vmem<C::WAIT_V>();  // (drained: all landed above)
     typedef typename std::conditional<F16, half4_t, f32x4>::type vvec_t;
 #pragma unroll
     for (int r = 0; r < kDecodeSub; ++r)
