@@ -373,6 +373,18 @@ int mi_hip_graph_prepare(const mi_cgraph* graph);
  * chain (no-ops); ATTN_KQV of a planned fused chain (the fused launch). */
 int mi_hip_compute_forward(mi_tensor* dst, int ith, int nth);
 
+/* Host-resident attention nodes (opt-in, default off): with on = 1,
+ * mi_hip_compute_forward also takes ATTN_QK, SOFTMAX and ATTN_KQV nodes that
+ * are not part of a fused chain on a bound KV cache -- e.g. a model whose
+ * head_dim the fused kernels do not cover (they take 64 and 128), so its
+ * cache stays on the host -- and runs each on the node kernels (bit-exact
+ * with src/ops_cpu.cpp:304-410): its sources are copied to a staging buffer
+ * (grown, and therefore allocated, to the largest node seen), the node runs,
+ * its output is copied back before the call returns. A correctness path for
+ * such models, not a throughput one. Process-wide. No counterpart in the
+ * reference. */
+int mi_hip_set_host_nodes(int32_t on);
+
 /* ---- read-bandwidth ceiling ---------------------------------------------- */
 
 /* The device counterpart of tools/bench_memread.cpp (the engine's read-only

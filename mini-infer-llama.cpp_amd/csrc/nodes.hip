@@ -9,12 +9,17 @@
 // multiply-add is formed) in the reference's order --
 // d ascending for scores, t ascending over all keys for the output -- so on
 // identical inputs they reproduce src/ops_cpu.cpp:356-380 and :386-410 bit
-// for bit. SOFTMAX uses the device expf and a tree sum, so it matches
-// src/ops_cpu.cpp:304-346 to rounding, not bitwise.
+// for bit. SOFTMAX reproduces src/ops_cpu.cpp:304-346 bit for bit too: the
+// glibc expf restated (libm_ref.h), the running sum as one rounded add per key
+// in key order, and the correctly rounded 1.0f / sum.
 #include "attn_common.h"
 #include "kernels.h"
+#define MI_LIBM_HD __host__ __device__
+#include "libm_ref.h"
 
 namespace mi {
+
+static __constant__ uint64_t kExpfTab[32] = MI_EXPF_TABLE;
 
 template <typename T>
 __device__ inline float ld(const NodeView& t, int64_t i0, int64_t i1, int64_t i2) {
@@ -42,7 +47,10 @@ __global__ void attn_qk_node_kernel(NodeView dst, NodeView q, NodeView k, int n_
 }
 
 // One wave per (token j, head h) row: causal scaled softmax over keys
-// [0, min(n_past + j + 1, n_kv)), zeros beyond.
+// [0, min(n_past + j + 1, n_kv)), zeros beyond. The maximum is order-free;
+// the sum follows the reference's order: per chunk of 64 keys every lane
+// computes and stores its e, then the wave adds the chunk's values one at a
+// time, lane k's k-th (a uniform running sum).
 __global__ void softmax_node_kernel(NodeView dst, NodeView src, int n_past, float scale) {
 #pragma clang fp contract(off)
   const int64_t n_kv = src.ne[0], n_tok = src.ne[1];
@@ -51,16 +59,27 @@ __global__ void softmax_node_kernel(NodeView dst, NodeView src, int n_past, floa
   const int64_t visible = min((int64_t)n_past + j + 1, n_kv);
   const int lane = threadIdx.x;
   float mx = -INFINITY;
-  for (int64_t i = lane; i < visible; i += kWave) mx = fmaxf(mx, ld<float>(src, i, j, h) * scale);
-  mx = wave_max(mx);
-  float sum = 0.f;
   for (int64_t i = lane; i < visible; i += kWave) {
-    const float e = expf(ld<float>(src, i, j, h) * scale - mx);
-    at(dst, i, j, h) = e;
-    sum += e;
+    const float v = ld<float>(src, i, j, h) * scale;
+    mx = v > mx ? v : mx;
   }
-  sum = wave_sum(sum);
-  const float inv = 1.f / sum;
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float o = __shfl_xor(mx, off);
+    mx = o > mx ? o : mx;
+  }
+  float sum = 0.f;
+  for (int64_t c = 0; c < visible; c += kWave) {
+    const int64_t i = c + lane;
+    float e = 0.f;
+    if (i < visible) {
+      e = expf_ref(ld<float>(src, i, j, h) * scale - mx, kExpfTab);
+      at(dst, i, j, h) = e;
+    }
+    const int n = (int)min<int64_t>(kWave, visible - c);
+    const int eb = __builtin_bit_cast(int, e);
+    for (int k = 0; k < n; ++k) sum = sum + __builtin_bit_cast(float, __builtin_amdgcn_readlane(eb, k));
+  }
+  const float inv = (float)(1.0 / (double)sum);  // the correctly rounded 1.0f / sum
   for (int64_t i = lane; i < visible; i += kWave) at(dst, i, j, h) = at(dst, i, j, h) * inv;
   for (int64_t i = visible + lane; i < n_kv; i += kWave) at(dst, i, j, h) = 0.f;
 }

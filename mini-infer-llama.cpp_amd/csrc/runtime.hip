@@ -81,6 +81,13 @@ struct State {
   std::atomic<int> decode_mode{MI_HIP_DECODE_AUTO};          // matrix cores of the decode kernel
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
   mi_hip_workspace* scratch_ws = nullptr;  // over the static scratch array (never freed)
+  // Host-resident attention nodes run on the node kernels (opt-in): a staging
+  // buffer that grows to the largest node seen, and a stream for it.
+  std::atomic<int> host_nodes{0};
+  std::mutex node_mu;
+  char* node_stage = nullptr;
+  size_t node_stage_bytes = 0;
+  hipStream_t node_stream = nullptr;
 };
 State g;
 
@@ -758,6 +765,14 @@ int mi_hip_shutdown(void) {
   g.default_ws = nullptr;
   ws_destroy(g.scratch_ws);  // the array itself stays until the process ends
   g.scratch_ws = nullptr;
+  {
+    std::lock_guard<std::mutex> nl(g.node_mu);
+    dev_free(g.node_stage, g.node_stage_bytes);
+    g.node_stage = nullptr;
+    g.node_stage_bytes = 0;
+    if (g.node_stream) (void)hipStreamDestroy(g.node_stream);
+    g.node_stream = nullptr;
+  }
   g.ready = false;
   g.device = -1;
   return MI_HIP_OK;
@@ -1368,6 +1383,73 @@ int mi_hip_graph_prepare(const mi_cgraph* graph) {
   return MI_HIP_OK;
 }
 
+namespace {
+
+// Bytes spanned by a tensor's elements from its data pointer.
+size_t tensor_extent(const mi_tensor* t) {
+  size_t e = t->type == MI_TYPE_F16 ? 2 : 4;
+  for (int i = 0; i < 4; ++i)
+    if (t->ne[i] > 1) e += (size_t)(t->ne[i] - 1) * t->nb[i];
+  return e;
+}
+
+// An ATTN_QK, SOFTMAX or ATTN_KQV node whose tensors live in host memory, run
+// on the node kernels: its sources are copied into the staging buffer, the
+// node runs on device copies of the three tensor headers, and the output is
+// copied back before returning (the caller's barrier then publishes it).
+int run_host_node(mi_tensor* dst) {
+  const int n_src = dst->op == MI_OP_SOFTMAX ? 1 : 2;
+  for (int i = 0; i < n_src; ++i)
+    if (!dst->src[i] || !dst->src[i]->data) return fail(MI_HIP_E_INVALID, "node source %d has no data", i);
+  if (!dst->data) return fail(MI_HIP_E_INVALID, "node output has no data");
+  size_t off[3], ext[3], total = 0;
+  const mi_tensor* ts[3] = {dst, dst->src[0], n_src > 1 ? dst->src[1] : nullptr};
+  for (int i = 0; i < 1 + n_src; ++i) {
+    ext[i] = tensor_extent(ts[i]);
+    off[i] = total;
+    total += (ext[i] + 255) & ~size_t(255);
+  }
+  int rc;
+  if ((rc = bind_device())) return rc;
+  std::lock_guard<std::mutex> lk(g.node_mu);
+  if (!g.node_stream) MI_TRY_HIP(hipStreamCreateWithFlags(&g.node_stream, hipStreamNonBlocking), "node stream");
+  if (total > g.node_stage_bytes) {
+    dev_free(g.node_stage, g.node_stage_bytes);
+    g.node_stage = nullptr;
+    g.node_stage_bytes = 0;
+    void* p = nullptr;
+    if ((rc = dev_alloc(&p, total, "host-node staging"))) return rc;
+    g.node_stage = static_cast<char*>(p);
+    g.node_stage_bytes = total;
+  }
+  mi_tensor dev[3];
+  for (int i = 0; i < 1 + n_src; ++i) {
+    dev[i] = *ts[i];
+    dev[i].data = g.node_stage + off[i];
+    if (i > 0)
+      MI_TRY_HIP(hipMemcpyAsync(dev[i].data, ts[i]->data, ext[i], hipMemcpyHostToDevice, g.node_stream),
+                 "node source copy");
+  }
+  dev[0].src[0] = &dev[1];
+  dev[0].src[1] = n_src > 1 ? &dev[2] : nullptr;
+  void* st = g.node_stream;
+  rc = dst->op == MI_OP_ATTN_QK ? mi_hip_op_attn_qk(&dev[0], st)
+       : dst->op == MI_OP_SOFTMAX ? mi_hip_op_softmax(&dev[0], st)
+                                  : mi_hip_op_attn_kqv(&dev[0], st);
+  if (rc) return rc;
+  MI_TRY_HIP(hipMemcpyAsync(dst->data, dev[0].data, ext[0], hipMemcpyDeviceToHost, g.node_stream), "node output copy");
+  MI_TRY_HIP(hipStreamSynchronize(g.node_stream), "node stream sync");
+  return MI_HIP_OK;
+}
+
+}  // namespace
+
+int mi_hip_set_host_nodes(int32_t on) {
+  if (on != 0 && on != 1) return fail(MI_HIP_E_INVALID, "on must be 0 or 1");
+  g.host_nodes.store(on);
+  return MI_HIP_OK;
+}
+
 int mi_hip_compute_forward(mi_tensor* dst, int ith, int nth) {
   (void)nth;
   if (!dst) return 0;
@@ -1410,7 +1492,9 @@ int mi_hip_compute_forward(mi_tensor* dst, int ith, int nth) {
                "chain (call mi_hip_graph_prepare after allocation)");
           return -1;
         }
-        return 0;
+        if (!g.host_nodes.load()) return 0;
+        if (ith != 0) return 1;
+        return run_host_node(dst) == MI_HIP_OK ? 1 : -1;
       }
       if (ith != 0) return 1;
       const mi_tensor* sm = dst->src[0];

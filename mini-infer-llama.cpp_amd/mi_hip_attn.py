@@ -176,6 +176,7 @@ SIGNATURES = {
     "mi_hip_set_deterministic": ([ctypes.c_int32], _I),
     "mi_hip_set_prefill_mode": ([ctypes.c_int32], _I),
     "mi_hip_set_decode_mode": ([ctypes.c_int32], _I),
+    "mi_hip_set_host_nodes": ([ctypes.c_int32], _I),
     "mi_hip_decode_tuning": ([ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32], _I),
     "mi_hip_kv_view": ([_P, _I, _I, ctypes.POINTER(ctypes.c_void_p),
                         ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_size_t)], _I),

@@ -16,7 +16,10 @@
 //                           -> then mi_hip_graph_prepare on the step's graph
 //   mi_kv_cache_init / _free (src/model_qwen2.cpp:557-605)
 //                           -> a device cache of the same shape, each layer's
-//                              host K/V tensor bound to it
+//                              host K/V tensor bound to it; for a head_dim the
+//                              fused kernels do not take, no device cache: the
+//                              attention nodes then run on the node kernels
+//                              (mi_hip_set_host_nodes)
 // The wrapped symbols are the reference's C++ names, so the wrappers carry
 // their mangled names (the Makefile lists the same names to --wrap).
 //
@@ -89,15 +92,24 @@ mi_kv_cache* __wrap__Z16mi_kv_cache_initRK16mi_qwen2_hparamsRK16mi_qwen2_weights
       __real__Z16mi_kv_cache_initRK16mi_qwen2_hparamsRK16mi_qwen2_weightsiRK20mi_threadpool_params(hp, w, n_ctx, tp);
   if (!kv) return kv;
   if (mi_hip_init(0) != MI_HIP_OK) die("mi_hip_init");
+  if (mi_hip_set_host_nodes(1) != MI_HIP_OK) die("mi_hip_set_host_nodes");
+  static std::once_flag once;
+  std::call_once(once, [] { std::atexit(report); });  // if the cache is never freed
   mi_hip_kv_desc d{hp.n_layer, n_ctx, hp.n_head_kv, hp.head_dim, hp.n_head, 0 /* F32 */};
   mi_hip_kv* hk = nullptr;
-  if (mi_hip_kv_create(&d, &hk) != MI_HIP_OK) die("mi_hip_kv_create");
+  const int crc = mi_hip_kv_create(&d, &hk);
+  if (crc == MI_HIP_E_UNSUPPORTED) {  // host cache; attention on the node kernels
+    std::fprintf(stderr, "mi_hip_hook: no device cache (%s)\n", mi_hip_last_error());
+    std::lock_guard<std::mutex> lk(g_mu);
+    mi_hip_alloc_stats st{};
+    if (mi_hip_get_alloc_stats(&st) == MI_HIP_OK) g_mallocs_at_init = st.n_malloc;
+    return kv;
+  }
+  if (crc != MI_HIP_OK) die("mi_hip_kv_create");
   for (int l = 0; l < hp.n_layer; l++) {
     if (mi_hip_kv_bind(hk, l, 0, kv->k[l]) != MI_HIP_OK) die("mi_hip_kv_bind K");
     if (mi_hip_kv_bind(hk, l, 1, kv->v[l]) != MI_HIP_OK) die("mi_hip_kv_bind V");
   }
-  static std::once_flag once;
-  std::call_once(once, [] { std::atexit(report); });  // if the cache is never freed
   std::lock_guard<std::mutex> lk(g_mu);
   g_caches[kv] = hk;
   mi_hip_alloc_stats st{};

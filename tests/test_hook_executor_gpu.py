@@ -16,6 +16,11 @@ node, views included (src/model_qwen2.cpp:647-672), for a batched prefill
 gallocr rewriting `extra` on every node and leaf each step
 (src/gallocr.cpp:94-95, 120-121), which the hook never reads.
 
+The reference's own tiny model (tests/golden/tiny_qwen2, head_dim 4: no device
+cache, so the hook runs its attention nodes on the node kernels through
+mi_hip_set_host_nodes) must reproduce the reference-held stage1 goldens bit
+for bit, prefill and decode, like the compiled reference itself does.
+
 Bars: logits within 0.05 of the unhooked CLI's at every prompt position and
 every incremental step (the fused attention is within 1e-4 of the CPU ops,
 and the Q8_0 activation rounding of the next layers turns any difference into
@@ -129,3 +134,17 @@ def test_thread_pool_generation(tiny):
     agree = next((i for i, (a, b) in enumerate(zip(got[1], want)) if a != b), len(want))
     print(f"hooked ids agree with the CPU engine's for {agree} of 64 steps", flush=True)
     assert got[1][0] == want[0]
+
+
+def test_reference_tiny_model_goldens_bit_for_bit(tmp_path):
+    # tests/test_graph.cpp:177-239's goldens, dumped by the reference CLI with
+    # every ATTN_QK / SOFTMAX / ATTN_KQV node run on the device node kernels
+    if not os.path.exists(HOOKED):
+        pytest.skip("oracle/_ref/mini_infer_hip is not built (the reference tree was absent)")
+    import test_tiny_qwen2_fixtures as fx
+    errs = fx.dump_and_compare(HOOKED, tmp_path)
+    for what, err, least in (("prefill", errs[0], 6), ("decode", errs[1], 12)):
+        assert "no device cache" in err, err[-500:]
+        allocs, nodes = hook_report(err)
+        print(f"{what}: attention nodes on device {nodes}", flush=True)
+        assert nodes >= least  # 3 attention nodes x 2 layers per forward call
