@@ -5,6 +5,9 @@ into tests/golden/tiny_qwen2/ and writes their sha256 manifest.
                                    2 layers, n_embd 8, 2 Q / 1 KV heads,
                                    head_dim 4; made by
                                    scripts/make_tiny_qwen2_fixture.py)
+  tiny_qwen2_q8_0.gguf             tests/fixtures/tiny_qwen2_q8_0.gguf (Q8_0
+                                   weights, n_embd 32, 1 head, head_dim 32;
+                                   tests/test_model_qwen2.cpp:241-288's model)
   stage1_golden_prefill/*.{bin,shape}
                                    the dump of a 5-token prefill of ids 0..4
   stage1_golden_decode/*.{bin,shape}
@@ -27,7 +30,7 @@ OUT = os.path.join(HERE, "tiny_qwen2")
 def main():
     src = os.path.join(REF, "tests", "fixtures")
     os.makedirs(OUT, exist_ok=True)
-    files = ["tiny_qwen2.gguf"]
+    files = ["tiny_qwen2.gguf", "tiny_qwen2_q8_0.gguf"]
     for d in ("stage1_golden_prefill", "stage1_golden_decode"):
         os.makedirs(os.path.join(OUT, d), exist_ok=True)
         for f in sorted(os.listdir(os.path.join(src, d))):

@@ -148,3 +148,22 @@ def test_reference_tiny_model_goldens_bit_for_bit(tmp_path):
         allocs, nodes = hook_report(err)
         print(f"{what}: attention nodes on device {nodes}", flush=True)
         assert nodes >= least  # 3 attention nodes x 2 layers per forward call
+
+
+def test_reference_q8_tiny_model_batch_equals_incremental(tmp_path):
+    # tests/test_model_qwen2.cpp:241-288 on the device: the Q8_0 tiny model
+    # (head_dim 32: attention on the node kernels) gives the same logits bits
+    # batched and one token per call, and the same bits as the unhooked CLI
+    if not (os.path.exists(HOOKED) and os.path.exists(PLAIN)):
+        pytest.skip("oracle/_ref/mini_infer{,_hip} are not built (the reference tree was absent)")
+    import test_tiny_qwen2_fixtures as fx
+    (tmp_path / "plain").mkdir()
+    (tmp_path / "hooked").mkdir()
+    pb, pi, _ = fx.batch_and_incremental(PLAIN, tmp_path / "plain")
+    hb, hi, errs = fx.batch_and_incremental(HOOKED, tmp_path / "hooked")
+    for err in errs:
+        allocs, nodes = hook_report(err)
+        assert nodes >= 3 * 2  # 3 attention nodes per layer, 2 layers
+    assert np.array_equal(hb.view(np.uint32), hi.view(np.uint32)), "batch vs incremental"
+    assert np.array_equal(hb.view(np.uint32), pb.view(np.uint32)), "hooked vs reference"
+    assert np.array_equal(hi.view(np.uint32), pi.view(np.uint32))

@@ -20,7 +20,7 @@ NAMES = ("embd", "layer_0", "layer_1", "output_norm", "logits")
 
 def test_fixture_copies_are_intact():
     man = json.load(open(os.path.join(FX, "manifest.json")))["sha256"]
-    assert "tiny_qwen2.gguf" in man and len(man) == 21
+    assert "tiny_qwen2.gguf" in man and "tiny_qwen2_q8_0.gguf" in man and len(man) == 22
     for f, h in man.items():
         assert hashlib.sha256(open(os.path.join(FX, f), "rb").read()).hexdigest() == h, f
 
@@ -55,3 +55,39 @@ def test_compiled_reference_reproduces_goldens(tmp_path):
     if not os.path.exists(PLAIN):
         pytest.skip("oracle/_ref/mini_infer is not built (the reference tree was absent)")
     dump_and_compare(PLAIN, tmp_path)
+
+
+Q8_TOKENS = "3 7 1 22 5"  # tests/test_model_qwen2.cpp:248
+
+
+def batch_and_incremental(exe, tmp_path, env=None):
+    """Logits of the Q8_0 tiny model for Q8_TOKENS: one batched prefill call
+    (--dump) and one token per call (--dump-incremental); returns both arrays
+    and the stderr of the two runs."""
+    idf = tmp_path / "q8.ids"
+    idf.write_text(Q8_TOKENS)
+    model = os.path.join(FX, "tiny_qwen2_q8_0.gguf")
+    out, errs = [], []
+    for flag in ("--dump", "--dump-incremental"):
+        d = tmp_path / flag.strip("-")
+        d.mkdir()
+        r = subprocess.run([exe, model, "--prompt-ids", str(idf), "-c", "16", flag, str(d)],
+                           capture_output=True, text=True, timeout=120, env=env)
+        assert r.returncode == 0, r.stderr[-2000:]
+        errs.append(r.stderr)
+        if flag == "--dump":
+            out.append(np.fromfile(d / "logits.bin", np.float32).reshape(5, -1))
+        else:
+            out.append(np.stack([np.fromfile(d / f"logits_step_{i}.bin", np.float32).reshape(-1)
+                                 for i in range(5)]))
+    return out[0], out[1], errs
+
+
+def test_compiled_reference_q8_batch_equals_incremental(tmp_path):
+    # tests/test_model_qwen2.cpp:241-288: zero mismatches between the batched
+    # and the token-by-token logits of the Q8_0 tiny model
+    if not os.path.exists(PLAIN):
+        pytest.skip("oracle/_ref/mini_infer is not built (the reference tree was absent)")
+    batch, incr, _ = batch_and_incremental(PLAIN, tmp_path)
+    assert batch.shape == (5, 64)
+    assert np.array_equal(batch.view(np.uint32), incr.view(np.uint32))
