@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--prefill-f32", action="store_true",
                     help="prefill products on v_mfma_f32_32x32x2f32 instead of split bf16 pairs")
     ap.add_argument("--only", default="",
-                    help="comma list: decode,sweep,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
+                    help="comma list: decode,streams,sweep,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
                          "counter calibration workload, only when named)")
     return ap.parse_args()
 
@@ -108,6 +108,71 @@ def bench_decode(torch, mh, lib, stream, steps, warmup, n_layers=24, n_kv=4096, 
     nbytes = decode_bytes(n_layers, n_kv, h, hkv, d, elt)
     return dict(ms_per_step=ms, kernel_ms=kern_ms, bytes=nbytes, sets=sets,
                 gbps=nbytes / (ms * 1e-3) / 1e9, kernel_gbps=nbytes / (kern_ms * 1e-3) / 1e9)
+
+
+def bench_decode_streams(torch, mh, lib, steps, warmup, n_streams=2, n_layers=24, n_kv=4096, h=14, hkv=2,
+                         d=64):
+    """The headline decode with independent batches alternating over n_streams
+    streams, each stream with its own decode workspace (so launches on
+    different streams may overlap): per-launch throughput when one launch's
+    start overlaps another's tail. The same kernels and work per launch; a
+    launch's workgroups are then not all resident at once, which the early
+    merge's bounded wait covers (its fallbacks are counted and reported)."""
+    sets = 2 * n_streams
+    gen = torch.Generator(device="cuda").manual_seed(4097)
+    streams = [torch.cuda.Stream() for _ in range(n_streams)]  # default priority
+    wss = [lib.workspace_create(hkv, h, d) for _ in range(n_streams)]
+    arrays = []
+    for s in range(sets):
+        st = streams[s % n_streams]
+        k = torch.randn((n_layers, n_kv, hkv, d), device="cuda", generator=gen)
+        v = torch.randn((n_layers, n_kv, hkv, d), device="cuda", generator=gen)
+        q = torch.randn((n_layers, 1, h, d), device="cuda", generator=gen)
+        o = torch.empty((n_layers, 1, h, d), device="cuda")
+        items = (mh.AttnArgs * n_layers)(*[
+            mh.attn_args(q[l], o[l], h // hkv, n_kv - 1, float(d) ** -0.5, st.cuda_stream, k=k[l], v=v[l],
+                         ws=wss[s % n_streams])
+            for l in range(n_layers)])
+        arrays.append((k, v, q, o, items))
+    torch.cuda.synchronize()
+
+    def launch(i):
+        rc = lib.mi_hip_attn_decode_batch(arrays[i % sets][4], n_layers, streams[i % n_streams].cuda_stream)
+        if rc:
+            raise mh.MiHipError(rc, lib.last_error())
+
+    try:
+        for i in range(warmup):
+            launch(i)
+        torch.cuda.synchronize()
+        for ws in wss:
+            lib.workspace_check(ws, streams[0].cuda_stream)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record(streams[0])
+        for st in streams[1:]:
+            st.wait_event(t0)
+        for i in range(steps):
+            launch(i)
+        for st in streams[1:]:
+            ev = torch.cuda.Event()
+            ev.record(st)
+            streams[0].wait_event(ev)
+        t1.record(streams[0])
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        fallbacks = lost = 0
+        for ws in wss:
+            rc, fb, lo = lib.workspace_check(ws, streams[0].cuda_stream)
+            fallbacks += fb
+            lost += lo
+    finally:
+        torch.cuda.synchronize()
+        for ws in wss:
+            lib.check(lib.mi_hip_workspace_destroy(ws))
+    nbytes = decode_bytes(n_layers, n_kv, h, hkv, d, 4)
+    return dict(streams=n_streams, us_per_launch=ms * 1e3, gbps=nbytes / (ms * 1e-3) / 1e9,
+                early_fallbacks=fallbacks, lost_groups=lost)
 
 
 def bench_decode_per_layer(torch, mh, lib, stream, steps, warmup, n_layers=24, n_kv=4096):
@@ -458,6 +523,10 @@ def main():
     res = {}
     if want("decode"):
         res["decode"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
+    if want("streams"):
+        res["streams"] = bench_decode_streams(torch, mh, lib, args.steps, args.warmup)
+        print(f"# decode 24x4096 over 2 streams: {res['streams']['gbps']:.1f} GB/s "
+              f"({res['streams']['us_per_launch']:.2f} us per launch)", file=sys.stderr, flush=True)
         print(f"# decode 24x4096: {res['decode']['gbps']:.1f} GB/s per step, kernel "
               f"{res['decode']['kernel_gbps']:.1f} GB/s", file=sys.stderr, flush=True)
     if want("sweep"):
@@ -623,6 +692,14 @@ def main():
                                 "frac": round(r["kernel_gbps"] / HBM_PEAK_GBPS, 4)}
     if "per_layer" in res:
         out["decode_per_layer_launch"] = {k: round(v, 3) for k, v in res["per_layer"].items()}
+    if "streams" in res:
+        sr = res["streams"]
+        out["decode_two_streams"] = {
+            "what": "the same 24 x 4096 launches alternating over two streams (independent batches, one "
+                    "workspace per stream): launches overlap, so one's start hides another's tail",
+            "us_per_launch": round(sr["us_per_launch"], 3), "gbps": round(sr["gbps"], 1),
+            "frac_of_8tbs": round(sr["gbps"] / 8000.0, 4), "early_fallbacks": sr["early_fallbacks"],
+            "lost_groups": sr["lost_groups"]}
     if "e2e" in res:
         out["e2e_qwen05_q8_0"] = res["e2e"]
     print(json.dumps(out))
