@@ -123,6 +123,11 @@ __device__ inline void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// Workgroup barrier that waits only for this wave's LDS operations: unlike
+// __syncthreads() it never makes the compiler drain vector-memory loads that
+// are still in flight (a ring's LDS-direct requests keep streaming across it).
+__device__ inline void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Loads and stores through the global address space. Pointers that reach a
 // kernel through LDS (a staged argument table) are otherwise generic, and a
 // generic (flat) access counts against both the vector-memory and the LDS
@@ -268,6 +273,59 @@ __device__ inline float ordered_sum(const float* sq, int n) {
     s = s + v.z;
     s = s + v.w;
   }
+  return s;
+}
+
+// The same sum over the N floats at LDS byte address sq (N a multiple of
+// 16; callers pad with +0.0, which leaves a sum of squares unchanged), for
+// one lane. The reads are issued as asm two chunks of 16 values ahead of the
+// additions, each chunk's wait tied to its registers: the chain of additions
+// does not wait for LDS, and the compiler neither reorders the reads nor
+// waits for LDS-direct requests elsewhere in LDS (it does not see the reads).
+namespace sum_lds {
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+template <int C>
+__device__ __forceinline__ void load(unsigned sq, f32x4_t (&d)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4 offset:%5\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %4 offset:%7\n\t"
+      "ds_read_b128 %3, %4 offset:%8"
+      : "=&v"(d[0]), "=&v"(d[1]), "=&v"(d[2]), "=&v"(d[3])
+      : "v"(sq), "n"(64 * C), "n"(64 * C + 16), "n"(64 * C + 32), "n"(64 * C + 48));
+}
+template <int K>
+__device__ __forceinline__ void wait(f32x4_t (&d)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(d[0]), "+v"(d[1]), "+v"(d[2]), "+v"(d[3]) : "n"(K));
+}
+template <int C, int KC>
+__device__ __forceinline__ void chunks(unsigned sq, f32x4_t (&b)[3][4], float& s) {
+#pragma clang fp contract(off)
+  if constexpr (C < KC) {
+    if constexpr (C + 2 < KC) load<C + 2>(sq, b[(C + 2) % 3]);
+    constexpr int later = KC - 1 - C < 2 ? KC - 1 - C : 2;  // chunks requested after this one
+    wait<4 * later>(b[C % 3]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      s = s + b[C % 3][u].x;
+      s = s + b[C % 3][u].y;
+      s = s + b[C % 3][u].z;
+      s = s + b[C % 3][u].w;
+    }
+    chunks<C + 1, KC>(sq, b, s);
+  }
+}
+}  // namespace sum_lds
+
+template <int N>
+__device__ __forceinline__ float ordered_sum_lds(const lds_t* sq) {
+  static_assert(N % 16 == 0 && N >= 32 && 4 * N <= 65536, "whole chunks of 16, offsets in range");
+  const unsigned a = (unsigned)(uintptr_t)sq;
+  sum_lds::f32x4_t b[3][4];
+  sum_lds::load<0>(a, b[0]);
+  sum_lds::load<1>(a, b[1]);
+  float s = 0.0f;
+  sum_lds::chunks<0, N / 16>(a, b, s);
   return s;
 }
 

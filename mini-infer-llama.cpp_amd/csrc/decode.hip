@@ -93,7 +93,6 @@ typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kSc1 = 16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
-__device__ inline void wg_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 template <int I, int N, typename F>
 __device__ __forceinline__ void static_for(F&& f) {

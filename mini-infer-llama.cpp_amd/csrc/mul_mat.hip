@@ -127,7 +127,21 @@ constexpr int kQ8Slot = 8 * kQ8RowBytesMax;
 constexpr int kQ8MaxBlocks = 30;                   // k <= 960
 constexpr int kQ8ActBytesMax = kQ8Cols * kQ8MaxBlocks * 36;
 constexpr int kQ8RingTake = kQ8RingWaves * 2 * kQ8Slot + kQ8ActBytesMax;  // the group counter
-constexpr int kQ8RingLds = kQ8RingTake + 16;
+constexpr int kQ8Scale = kQ8RingTake + 16;        // the norm scale of each column
+constexpr int kQ8RingLds = kQ8Scale + 4 * kQ8Cols;
+constexpr int kQ8XOff = kQ8RingLds;                // one F32 column (M = 1), past the ring
+constexpr int kQ8RingLdsAll = kQ8XOff + kQ8MaxBlocks * 32 * 4;
+
+// A float load the compiler does not track, so that it cannot make the
+// products wait for it (its register allocation otherwise sometimes reuses
+// the destination's neighbour at once); landed(v) waits for every load of
+// the wave (vmcnt 0) and ties v to that wait, so nothing reads v earlier.
+__device__ inline float load_f32_async(const char* p) {
+  float v;
+  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ inline void landed(float& v) { asm volatile("s_waitcnt vmcnt(0)" : "+v"(v)::"memory"); }
 
 // Returns *c and adds 1 (an LDS atomic). As asm: the compiler's wait insertion
 // would otherwise wait for every LDS-direct load in flight (vmcnt(0)) before
@@ -151,38 +165,6 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
   const int nblk = (int)(p.k / 32);
   const int abytes = nblk * 36;
   char* const act_lds = ring_lds + kQ8RingWaves * 2 * kQ8Slot;
-  if (!p.x) {
-    for (int i = threadIdx.x; i < M * abytes / 4; i += kQ8RingWaves * kWave) {
-      const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
-      *reinterpret_cast<unsigned*>(act_lds + c * abytes + o) = gload<unsigned>(p.a + c * p.a_nb1 + o);
-    }
-  } else {
-    // the prologue: columns into LDS (the ring slots are free until the first
-    // refill), the norm's ordered sums, then one thread per element in groups
-    // of 32 lanes forming each block
-    __shared__ float s_scale[kQ8Cols];
-    float* const xs = reinterpret_cast<float*>(ring_lds);
-    float* const sq = xs + M * p.k;
-    const int k = (int)p.k;
-    for (int i = threadIdx.x; i < M * k; i += kQ8RingWaves * kWave) {
-      const int c = i / k;
-      const float v = gload<float>(p.x + c * p.x_ld + (i - c * k));
-      xs[i] = v;
-      sq[i] = v * v;
-    }
-    __syncthreads();
-    if (p.norm_w && threadIdx.x < M) s_scale[threadIdx.x] = rms_scale(ordered_sum(sq + threadIdx.x * k, k), k, p.eps);
-    __syncthreads();
-    for (int i = threadIdx.x; i < M * k; i += kQ8RingWaves * kWave) {
-      const int c = i / k, e = i - c * k;
-      const float y = p.norm_w ? (xs[i] * s_scale[c]) * gload<float>(p.norm_w + e) : xs[i];
-      float d;
-      const int q = q8_lane_quant(y, d);
-      char* blk = act_lds + c * abytes + 36 * (e / 32);
-      if ((e & 31) == 0) *reinterpret_cast<float*>(blk) = d;
-      blk[4 + (e & 31)] = (char)q;
-    }
-  }
   // This workgroup's contiguous range of 8-row groups; its waves take groups
   // from an LDS counter as they refill, so a wave served faster takes more
   // and the waves finish together.
@@ -210,19 +192,116 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     for (int i = 0; i < 8; ++i) dma16(r, slots + s * kQ8Slot + 1024 * i, (unsigned)(1024 * i + 16 * lane));
     return live ? g : -1;
   };
-  if (threadIdx.x == 0) *reinterpret_cast<__attribute__((address_space(3))) unsigned*>(take) = 0u;
-  __syncthreads();  // the activation is staged (before the ring requests: the barrier waits for all loads)
-  int64_t g_0 = refill(0), g_1 = refill(1);  // the group in each slot, or -1
+  int64_t g_0, g_1;  // the group in each slot, or -1
+  // LDS read through lds_t pointers into the regions past the ring: the
+  // compiler then sees that they cannot overlap the ring's LDS-direct
+  // requests and does not wait for those before reading
+  lds_t* const s_scale = lds + kQ8Scale;
+  if constexpr (M == 1) {
+    // One column: its loads go into registers (at most 2 elements, or 1
+    // activation word, per thread: k <= 960), the ring's first requests
+    // follow, and the prologue's arithmetic runs under their latency. The
+    // column's squares are staged past the ring for the norm's ordered sum.
+    constexpr int kT = kQ8RingWaves * kWave;
+    const int t = threadIdx.x;
+    const int k = (int)p.k;
+    float xv[2] = {0.0f, 0.0f}, nw[2] = {1.0f, 1.0f};
+    unsigned av = 0;
+    if (p.x) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        if (t + kT * j < k) {
+          xv[j] = gload<float>(p.x + t + kT * j);
+          if (p.norm_w) nw[j] = gload<float>(p.norm_w + t + kT * j);
+        }
+    } else if (t < abytes / 4) {
+      av = gload<unsigned>(p.a + 4 * t);
+    }
+    if (t == 0) *take = 0u;
+    wg_barrier();  // the counter is zero (the loads above stay in flight)
+    g_0 = refill(0);
+    g_1 = refill(1);
+    if (!p.x) {
+      if (t < abytes / 4) *reinterpret_cast<unsigned*>(act_lds + 4 * t) = av;
+    } else {
+      float scale = 1.0f;
+      if (p.norm_w) {
+        // the squares, padded with +0.0 to kQ8MaxBlocks * 32
+        lds_t* const sq = lds + kQ8XOff;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          if (t + kT * j < kQ8MaxBlocks * 32) lds_store<float>(sq + 4 * (t + kT * j), t + kT * j < k ? xv[j] * xv[j] : 0.0f);
+        wg_barrier();
+        if (t == 0) lds_store<float>(s_scale, rms_scale(ordered_sum_lds<kQ8MaxBlocks * 32>(sq), k, p.eps));
+        wg_barrier();
+        scale = lds_load<float>(s_scale);
+      }
+      // one thread per element in groups of 32 lanes forming each block (k
+      // and kT are multiples of 32, so a group is active as a whole)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int e = t + kT * j;
+        if (e < k) {
+          const float y = p.norm_w ? (xv[j] * scale) * nw[j] : xv[j];
+          float d;
+          const int q = q8_lane_quant(y, d);
+          char* blk = act_lds + 36 * (e / 32);
+          if ((e & 31) == 0) *reinterpret_cast<float*>(blk) = d;
+          blk[4 + (e & 31)] = (char)q;
+        }
+      }
+    }
+    wg_barrier();  // the activation is staged
+  } else {
+    if (!p.x) {
+      for (int i = threadIdx.x; i < M * abytes / 4; i += kQ8RingWaves * kWave) {
+        const int c = i / (abytes / 4), o = 4 * (i - c * (abytes / 4));
+        *reinterpret_cast<unsigned*>(act_lds + c * abytes + o) = gload<unsigned>(p.a + c * p.a_nb1 + o);
+      }
+    } else {
+      // the prologue: columns into LDS (the ring slots are free until the
+      // first refill), the norm's ordered sums, then one thread per element
+      // in groups of 32 lanes forming each block
+      float* const xs = reinterpret_cast<float*>(ring_lds);
+      float* const sq = xs + M * p.k;
+      const int k = (int)p.k;
+      for (int i = threadIdx.x; i < M * k; i += kQ8RingWaves * kWave) {
+        const int c = i / k;
+        const float v = gload<float>(p.x + c * p.x_ld + (i - c * k));
+        xs[i] = v;
+        sq[i] = v * v;
+      }
+      __syncthreads();
+      if (p.norm_w && threadIdx.x < M)
+        lds_store<float>(s_scale + 4 * threadIdx.x, rms_scale(ordered_sum(sq + threadIdx.x * k, k), k, p.eps));
+      __syncthreads();
+      for (int i = threadIdx.x; i < M * k; i += kQ8RingWaves * kWave) {
+        const int c = i / k, e = i - c * k;
+        const float y = p.norm_w ? (xs[i] * lds_load<float>(s_scale + 4 * c)) * gload<float>(p.norm_w + e) : xs[i];
+        float d;
+        const int q = q8_lane_quant(y, d);
+        char* blk = act_lds + c * abytes + 36 * (e / 32);
+        if ((e & 31) == 0) *reinterpret_cast<float*>(blk) = d;
+        blk[4 + (e & 31)] = (char)q;
+      }
+    }
+    if (threadIdx.x == 0) *take = 0u;
+    __syncthreads();  // the activation is staged (before the ring requests: the barrier waits for all loads)
+    g_0 = refill(0);
+    g_1 = refill(1);
+  }
   const int l = lane & 7, rs = lane >> 3;
   const lds_t* const act = lds + kQ8RingWaves * 2 * kQ8Slot;
   // one column: this lane's activation byte groups and the block scales, in registers
   float a_d[M == 1 ? kQ8MaxBlocks : 1];
   int a_q[M == 1 ? kQ8MaxBlocks : 1];
   if constexpr (M == 1) {
+    // every block of the region (those past the row are never added): reads
+    // without branches, so they are all in flight together
 #pragma unroll
     for (int b = 0; b < kQ8MaxBlocks; ++b) {
-      a_d[b] = b < nblk ? lds_load<float>(act + 36 * b) : 0.f;
-      a_q[b] = b < nblk ? lds_load<int>(act + 36 * b + 4 + 4 * l) : 0;
+      a_d[b] = lds_load<float>(act + 36 * b);
+      a_q[b] = lds_load<int>(act + 36 * b + 4 + 4 * l);
     }
   }
   // slots in turn until the first empty one (a wave's takes increase, so
@@ -235,6 +314,15 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     else
       wait_vmem<M + 8>();
     const lds_t* const w = lds + (wv * 2 + s) * kQ8Slot + rs * (int)p.w_nb1;
+    const int64_t row = g * 8 + rs;
+    // the optional added term, requested before the products so that its
+    // latency overlaps them
+    float addv[M];
+    if (p.add) {
+      const int64_t ra = min(row, p.n - 1);  // every lane loads
+#pragma unroll
+      for (int c = 0; c < M; ++c) addv[c] = load_f32_async(p.add + ra * p.add_nb0 + c * p.add_nb1);
+    }
     float acc[M];
 #pragma unroll
     for (int c = 0; c < M; ++c) acc[c] = 0.0f;
@@ -256,7 +344,6 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
         acc[c] = b < nblk ? r : acc[c];
       }
     }
-    const int64_t row = g * 8 + rs;
 #pragma unroll
     for (int c = 0; c < M; ++c) {
       float t = acc[c] + __shfl_xor(acc[c], 4, 8);
@@ -264,14 +351,15 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       t = t + __shfl_xor(t, 2, 8);
       acc[c] = t;
     }
-    // the optional added term: its loads finish (vmcnt 0, which also drains
-    // the other slot's refill) before the stores, so the fixed waits still
-    // count exactly M stores and 8 loads per iteration
+    // the added term's loads finish (vmcnt 0, which also drains the other
+    // slot's refill) before the stores, so the fixed waits still count
+    // exactly M stores and 8 loads per iteration
     if (p.add) {
 #pragma unroll
-      for (int c = 0; c < M; ++c)
-        if (row < p.n && l == 0) acc[c] = acc[c] + gload<float>(p.add + row * p.add_nb0 + c * p.add_nb1);
-      wait_vmem<0>();
+      for (int c = 0; c < M; ++c) {
+        landed(addv[c]);
+        if (row < p.n && l == 0) acc[c] = acc[c] + addv[c];
+      }
     }
     // RoPE epilogue (one column): the rotation partner is row rs ^ 1 of this
     // group, 8 lanes away; the destination is chosen per lane, so it is still
@@ -381,7 +469,12 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
                             gload<unsigned>(p.a + (c0 + c) * p.a_nb1 + o));
       }
     }
-    wait_vmem<0>();  // the LDS-direct transfers have landed
+    // one column: the added term is requested now, so its latency overlaps
+    // the transfers'
+    float addv = 0.0f;
+    if (MC == 1 && p.add) addv = load_f32_async(p.add + min(row, p.n - 1) * p.add_nb0 + c0 * p.add_nb1);
+    wait_vmem<0>();  // the LDS-direct transfers (and the added term) have landed
+    if (MC == 1 && p.add) landed(addv);
     if (c0 == 0 && wb4 != wbytes && lane == 0)
       lds_store<unsigned short>((lds_t*)(stage_lds + wb4), gload<unsigned short>(wsrc + wb4));
     __syncthreads();
@@ -429,7 +522,7 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
         s = s + __shfl_xor(s, 1, 8);
         s = s + __shfl_xor(s, 2, 8);
         if (live && l == 0) {
-          if (p.add) s = s + gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1);
+          if (p.add) s = s + (MC == 1 ? addv : gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1));
           gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
         }
       }
@@ -473,14 +566,14 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) 
       for (int v = 0; v < 2; ++v)
         for (int m = 0; m < kQ8Cols; ++m)
           if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)fns[v][m], hipFuncAttributeMaxDynamicSharedMemorySize, kQ8RingLds);
+            e = hipFuncSetAttribute((const void*)fns[v][m], hipFuncAttributeMaxDynamicSharedMemorySize, kQ8RingLdsAll);
       return e;
     }();
     if (attr != hipSuccess) return attr;
     const int64_t groups = (p.n + 7) / 8;
     const unsigned grid = (unsigned)std::min<int64_t>(n_cu > 0 ? n_cu : 256, (groups + kQ8RingWaves - 1) / kQ8RingWaves);
     const bool epi = p.rope_on || p.perm_hd;
-    hipLaunchKernelGGL(fns[epi ? 1 : 0][p.m - 1], dim3(grid), dim3(kQ8RingWaves * kWave), kQ8RingLds, stream, p);
+    hipLaunchKernelGGL(fns[epi ? 1 : 0][p.m - 1], dim3(grid), dim3(kQ8RingWaves * kWave), kQ8RingLdsAll, stream, p);
   } else if (q8_stage_lds_bytes(p.w_nb1, p.k) <= kQ8StageLdsMax &&
              reinterpret_cast<uintptr_t>(p.w) % 16 == 0 && (8 * p.w_nb1) % 16 == 0 &&
              p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0) {
