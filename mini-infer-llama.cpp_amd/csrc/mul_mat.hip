@@ -132,16 +132,29 @@ constexpr int kQ8RingLds = kQ8Scale + 4 * kQ8Cols;
 constexpr int kQ8XOff = kQ8RingLds;                // one F32 column (M = 1), past the ring
 constexpr int kQ8RingLdsAll = kQ8XOff + kQ8MaxBlocks * 32 * 4;
 
-// A float load the compiler does not track, so that it cannot make the
-// products wait for it (its register allocation otherwise sometimes reuses
-// the destination's neighbour at once); landed(v) waits for every load of
-// the wave (vmcnt 0) and ties v to that wait, so nothing reads v earlier.
-__device__ inline float load_f32_async(const char* p) {
-  float v;
-  asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(p) : "memory");
+// A load of two floats that the compiler does not track, so that it never
+// makes the products wait for it (its register allocation otherwise sometimes
+// reuses a register of the pending load at once); landed(v) waits for every
+// load of the wave (vmcnt 0) and ties v to that wait, so nothing reads v
+// earlier. Issue it on every path: a branch around it could make the compiler
+// copy the register before the data has landed.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ inline f32x2_t load_f32x2_async(const float* p) {
+  f32x2_t v;
+  asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(v) : "v"(p) : "memory");
   return v;
 }
-__device__ inline void landed(float& v) { asm volatile("s_waitcnt vmcnt(0)" : "+v"(v)::"memory"); }
+__device__ inline void landed(f32x2_t& v) { asm volatile("s_waitcnt vmcnt(0)" : "+v"(v)::"memory"); }
+// vmcnt(BASE + extra) for extra in [0, 2] (a uniform value)
+template <int BASE>
+__device__ inline void wait_vmem_plus(int extra) {
+  if (extra == 0)
+    wait_vmem<BASE>();
+  else if (extra == 1)
+    wait_vmem<BASE + 1>();
+  else
+    wait_vmem<BASE + 2>();
+}
 
 // Returns *c and adds 1 (an LDS atomic). As asm: the compiler's wait insertion
 // would otherwise wait for every LDS-direct load in flight (vmcnt(0)) before
@@ -176,8 +189,10 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
   const int64_t total = p.n * p.w_nb1;
   const rsrc_t none = make_rsrc(p.w, 0u);
   lds_t* const slots = lds + wv * 2 * kQ8Slot;
-  // refills slot s with the next group taken; returns it, or -1 past the range
-  auto refill = [&](int s) __attribute__((always_inline)) -> int64_t {
+  // refills slot s with the next group taken; returns it, or -1 past the
+  // range (with issue_dead, a take past the range still issues its 8
+  // zero-sized requests, keeping the number of loads per refill fixed)
+  auto refill = [&](int s, bool issue_dead) __attribute__((always_inline)) -> int64_t {
     unsigned t = 0;
     if (lane == 0) t = lds_take(take);
     t = (unsigned)__builtin_amdgcn_readfirstlane((int)t);
@@ -188,8 +203,10 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       const int64_t start = g * 8 * p.w_nb1;
       r = make_rsrc(p.w + start, (unsigned)min<int64_t>(8 * p.w_nb1, total - start));
     }
+    if (live || issue_dead) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) dma16(r, slots + s * kQ8Slot + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+      for (int i = 0; i < 8; ++i) dma16(r, slots + s * kQ8Slot + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+    }
     return live ? g : -1;
   };
   int64_t g_0, g_1;  // the group in each slot, or -1
@@ -218,9 +235,17 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       av = gload<unsigned>(p.a + 4 * t);
     }
     if (t == 0) *take = 0u;
+    // the region's blocks past the row are zero: their products add exactly
+    // +0.0 (the weight block read for them is a real one, so its scale is
+    // finite, and a sum is never -0.0), so no block needs a select
+    for (int i = t; i < (kQ8MaxBlocks - nblk) * 9; i += kT)
+      *reinterpret_cast<unsigned*>(act_lds + abytes + 4 * i) = 0u;
     wg_barrier();  // the counter is zero (the loads above stay in flight)
-    g_0 = refill(0);
-    g_1 = refill(1);
+    // both slots are requested even for an empty take: the compiler then
+    // knows that exactly 16 requests follow the loads above, and waits for
+    // those loads with vmcnt(16)
+    g_0 = refill(0, true);
+    g_1 = refill(1, true);
     if (!p.x) {
       if (t < abytes / 4) *reinterpret_cast<unsigned*>(act_lds + 4 * t) = av;
     } else {
@@ -287,8 +312,8 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     }
     if (threadIdx.x == 0) *take = 0u;
     __syncthreads();  // the activation is staged (before the ring requests: the barrier waits for all loads)
-    g_0 = refill(0);
-    g_1 = refill(1);
+    g_0 = refill(0, true);
+    g_1 = refill(1, true);
   }
   const int l = lane & 7, rs = lane >> 3;
   const lds_t* const act = lds + kQ8RingWaves * 2 * kQ8Slot;
@@ -296,8 +321,8 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
   float a_d[M == 1 ? kQ8MaxBlocks : 1];
   int a_q[M == 1 ? kQ8MaxBlocks : 1];
   if constexpr (M == 1) {
-    // every block of the region (those past the row are never added): reads
-    // without branches, so they are all in flight together
+    // every block of the region, read without branches so that the reads
+    // are all in flight together (the blocks past the row are zero)
 #pragma unroll
     for (int b = 0; b < kQ8MaxBlocks; ++b) {
       a_d[b] = lds_load<float>(act + 36 * b);
@@ -309,19 +334,41 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
   for (int s = 0, it = 0;; s ^= 1, ++it) {
     const int64_t g = s ? g_1 : g_0;
     if (g < 0) break;
-    if (it == 0)
-      wait_vmem<8>();
-    else
-      wait_vmem<M + 8>();
     const lds_t* const w = lds + (wv * 2 + s) * kQ8Slot + rs * (int)p.w_nb1;
     const int64_t row = g * 8 + rs;
-    // the optional added term, requested before the products so that its
-    // latency overlaps them
+    // the optional added term (and, for the RoPE epilogue, the row's cos/sin
+    // pair): with one column requested before the slot's wait, so that their
+    // latency overlaps it and the products; counted in that wait (extra).
+    // Every lane loads, from a row inside the tensor. The pair is an asm load
+    // issued on every path (no branch, so the compiler never copies its
+    // register before landed() waits for it); its wait drains the wave.
     float addv[M];
-    if (p.add) {
-      const int64_t ra = min(row, p.n - 1);  // every lane loads
+    f32x2_t csv;
+    int extra = 0;
+    if constexpr (M == 1) {
+      if (p.add) {
+        addv[0] = gload<float>(p.add + min(row, p.n - 1) * p.add_nb0);
+        ++extra;
+      }
+      if constexpr (EPI) {
+        const RopeEpi& re = p.rope;
+        const int64_t pair = p.rope_on ? (int64_t)re.pos * (re.hd / 2) + (row % re.hd) / 2 : 0;
+        csv = load_f32x2_async(p.rope_on ? re.cs + 2 * pair : reinterpret_cast<const float*>(p.w));
+        ++extra;
+      }
+    }
+    if (it == 0)
+      wait_vmem_plus<8>(extra);
+    else
+      wait_vmem_plus<M + 8>(extra);
+    if constexpr (M > 1) {
+      // more columns: requested after the wait, their latency overlapping
+      // the products
+      if (p.add) {
+        const int64_t ra = min(row, p.n - 1);
 #pragma unroll
-      for (int c = 0; c < M; ++c) addv[c] = load_f32_async(p.add + ra * p.add_nb0 + c * p.add_nb1);
+        for (int c = 0; c < M; ++c) addv[c] = gload<float>(p.add + ra * p.add_nb0 + c * p.add_nb1);
+      }
     }
     float acc[M];
 #pragma unroll
@@ -341,7 +388,7 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
         const int aq = M == 1 ? a_q[b] : lds_load<int>(act + c * abytes + 36 * bb + 4 + 4 * l);
         const int isum = __builtin_amdgcn_sdot4(wq, aq, 0, false);
         const float r = __builtin_fmaf((float)isum, dxdy, acc[c]);
-        acc[c] = b < nblk ? r : acc[c];
+        acc[c] = M == 1 || b < nblk ? r : acc[c];
       }
     }
 #pragma unroll
@@ -355,12 +402,12 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     // slot's refill) before the stores, so the fixed waits still count
     // exactly M stores and 8 loads per iteration
     if (p.add) {
+      wait_vmem<0>();
 #pragma unroll
-      for (int c = 0; c < M; ++c) {
-        landed(addv[c]);
+      for (int c = 0; c < M; ++c)
         if (row < p.n && l == 0) acc[c] = acc[c] + addv[c];
-      }
     }
+    if constexpr (EPI && M == 1) landed(csv);
     // RoPE epilogue (one column): the rotation partner is row rs ^ 1 of this
     // group, 8 lanes away; the destination is chosen per lane, so it is still
     // one store instruction
@@ -373,9 +420,8 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
         const int64_t h = row / re.hd;  // head (Q heads, then K heads, then V heads)
         const int w = (int)(row - h * re.hd);
         if (row < qk_rows) {
-          const float2 cs = *reinterpret_cast<const float2*>(re.cs + 2 * ((int64_t)re.pos * (re.hd / 2) + (w >> 1)));
           const float x0 = (w & 1) ? other : acc[0], x1 = (w & 1) ? acc[0] : other;
-          acc[0] = (w & 1) ? x0 * cs.y + x1 * cs.x : x0 * cs.x - x1 * cs.y;
+          acc[0] = (w & 1) ? x0 * csv.y + x1 * csv.x : x0 * csv.x - x1 * csv.y;
         }
         const int d = row < qk_rows ? (w >> 1) + (w & 1) * (re.hd / 2) : w;
         if (row < re.n_q)
@@ -396,7 +442,7 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
                                   : reinterpret_cast<float*>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + c * p.dst_nb1);
       if (row < p.n && l == 0) gstore<float>(o, acc[c]);
     }
-    const int64_t gn = refill(s);
+    const int64_t gn = refill(s, true);
     if (s)
       g_1 = gn;
     else
@@ -472,9 +518,8 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
     // one column: the added term is requested now, so its latency overlaps
     // the transfers'
     float addv = 0.0f;
-    if (MC == 1 && p.add) addv = load_f32_async(p.add + min(row, p.n - 1) * p.add_nb0 + c0 * p.add_nb1);
+    if (MC == 1 && p.add) addv = gload<float>(p.add + min(row, p.n - 1) * p.add_nb0 + c0 * p.add_nb1);
     wait_vmem<0>();  // the LDS-direct transfers (and the added term) have landed
-    if (MC == 1 && p.add) landed(addv);
     if (c0 == 0 && wb4 != wbytes && lane == 0)
       lds_store<unsigned short>((lds_t*)(stage_lds + wb4), gload<unsigned short>(wsrc + wb4));
     __syncthreads();
