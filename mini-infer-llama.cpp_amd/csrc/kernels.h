@@ -118,6 +118,13 @@ struct Q8MulMat {
   int64_t x_ld = 0;
   const float* norm_w = nullptr;
   float eps = 0.0f;
+  // Optional SwiGLU epilogue (streaming form, one column, q8_swiglu_out_ok):
+  // the rows are gate/up pairs (row 2i is gate_i, row 2i + 1 is up_i), and
+  // instead of F32 rows the kernel writes SiLU(gate_i) * up_i as Q8_0_ACT
+  // blocks (block j, elements 32 j .. 32 j + 31, at swiglu_out + 36 j) -- the
+  // engine's SILU, MUL and QUANTIZE nodes after the FFN gate/up projections
+  // (src/model_qwen2.cpp:188-189, src/ops_cpu.cpp:412) fused.
+  char* swiglu_out = nullptr;
   // Rows of the first perm_rows permuted within heads of perm_hd rows as
   // RopeEpi describes; the stores put them back in natural order (0: none).
   int32_t perm_hd = 0;
@@ -137,6 +144,10 @@ __host__ __device__ inline int64_t q8_unperm_row(int64_t r, int32_t hd, int64_t 
 // Whether launch_mul_mat_q8_0 takes the streaming form for p (the only form
 // with the activation prologue).
 bool q8_ring_form(const Q8MulMat& p);
+// Whether launch_mul_mat_q8_0 can run p with its SwiGLU epilogue (the
+// streaming form, one column, no added term or RoPE, n a multiple of 64 and
+// at most one workgroup per 64 rows on the device).
+bool q8_swiglu_out_ok(const Q8MulMat& p, int n_cu);
 hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream);
 hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream);
 

@@ -42,8 +42,11 @@
 
 namespace mi {
 
-// tab: the 32 MI_EXPF_TABLE entries (device code passes a __constant__ copy).
-MI_LIBM_HD inline float expf_ref(float x, const uint64_t* tab) {
+// tab: the 32 MI_EXPF_TABLE entries (any pointer type: device code passes a
+// __constant__ copy, or an LDS copy when its reads must not wait on global
+// memory).
+template <typename Tab>
+MI_LIBM_HD inline float expf_ref(float x, Tab tab) {
   const double inv_ln2_n = 0x1.71547652b82fep+0 * 32;
   const double shift = 0x1.8p+52;
   const double c0 = 0x1.c6af84b912394p-5 / (32.0 * 32.0 * 32.0);

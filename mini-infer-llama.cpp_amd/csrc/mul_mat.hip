@@ -22,7 +22,21 @@
 #include "attn_common.h"
 #include "kernels.h"
 
+#define MI_LIBM_HD __host__ __device__
+#include "libm_ref.h"
+
 namespace mi {
+namespace {
+__constant__ uint64_t kExpfTab[32] = MI_EXPF_TABLE;
+}  // namespace
+
+// SiLU(g) * u as the engine computes it: g / (1 + expf(-g)) with the host C
+// library's expf (libm_ref.h, its table at tab), then the product.
+template <typename Tab>
+__device__ inline float swiglu_value(float g, float u, Tab tab) {
+#pragma clang fp contract(off)
+  return (g / (1.0f + expf_ref(-g, tab))) * u;
+}
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
@@ -130,7 +144,9 @@ constexpr int kQ8RingTake = kQ8RingWaves * 2 * kQ8Slot + kQ8ActBytesMax;  // the
 constexpr int kQ8Scale = kQ8RingTake + 16;        // the norm scale of each column
 constexpr int kQ8RingLds = kQ8Scale + 4 * kQ8Cols;
 constexpr int kQ8XOff = kQ8RingLds;                // one F32 column (M = 1), past the ring
-constexpr int kQ8RingLdsAll = kQ8XOff + kQ8MaxBlocks * 32 * 4;
+constexpr int kQ8SwTab = kQ8XOff + kQ8MaxBlocks * 32 * 4;  // SwiGLU epilogue: expf's table
+constexpr int kQ8SwVals = kQ8SwTab + 32 * 8;                 // and the workgroup's 32 values
+constexpr int kQ8RingLdsAll = kQ8SwVals + 32 * 4;
 
 // A load of two floats that the compiler does not track, so that it never
 // makes the products wait for it (its register allocation otherwise sometimes
@@ -145,15 +161,17 @@ __device__ inline f32x2_t load_f32x2_async(const float* p) {
   return v;
 }
 __device__ inline void landed(f32x2_t& v) { asm volatile("s_waitcnt vmcnt(0)" : "+v"(v)::"memory"); }
-// vmcnt(BASE + extra) for extra in [0, 2] (a uniform value)
+// vmcnt(BASE + extra) for extra in [0, 3] (a uniform value)
 template <int BASE>
 __device__ inline void wait_vmem_plus(int extra) {
   if (extra == 0)
     wait_vmem<BASE>();
   else if (extra == 1)
     wait_vmem<BASE + 1>();
-  else
+  else if (extra == 2)
     wait_vmem<BASE + 2>();
+  else
+    wait_vmem<BASE + 3>();
 }
 
 // Returns *c and adds 1 (an LDS atomic). As asm: the compiler's wait insertion
@@ -224,6 +242,9 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     const int k = (int)p.k;
     float xv[2] = {0.0f, 0.0f}, nw[2] = {1.0f, 1.0f};
     unsigned av = 0;
+    // the SwiGLU epilogue reads expf's table from LDS (a read of the
+    // __constant__ one is a global load, whose wait would drain the ring)
+    const uint64_t te = p.swiglu_out ? kExpfTab[lane & 31] : 0;
     if (p.x) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -276,7 +297,8 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
         }
       }
     }
-    wg_barrier();  // the activation is staged
+    if (p.swiglu_out && t < 32) lds_store<uint64_t>(lds + kQ8SwTab + 8 * t, te);
+    wg_barrier();  // the activation (and expf's table) is staged
   } else {
     if (!p.x) {
       for (int i = threadIdx.x; i < M * abytes / 4; i += kQ8RingWaves * kWave) {
@@ -357,7 +379,10 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
         ++extra;
       }
     }
+    // (the SwiGLU epilogue issues no stores: it writes LDS)
     if (it == 0)
+      wait_vmem_plus<8>(extra);
+    else if (M == 1 && p.swiglu_out)
       wait_vmem_plus<8>(extra);
     else
       wait_vmem_plus<M + 8>(extra);
@@ -435,12 +460,22 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     // the slot's reads are done before it is refilled; then M stores (row 0
     // of a group always exists, so every store instruction issues), 8 loads
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (M == 1 && p.swiglu_out) {
+      // gate rows are even, their up rows 8 lanes away: the group's 4 values
+      // go to the workgroup's block in LDS (the workgroup's groups are the
+      // block's 8)
+      const float up = __shfl_xor(acc[0], 8);
+      if ((rs & 1) == 0 && l == 0)
+        lds_store<float>(lds + kQ8SwVals + 4 * (4 * (int)(g - glo) + (rs >> 1)),
+                         swiglu_value(acc[0], up, (const __attribute__((address_space(3))) uint64_t*)(lds + kQ8SwTab)));
+    } else {
 #pragma unroll
     for (int c = 0; c < M; ++c) {
       float* const o = !EPI ? reinterpret_cast<float*>(p.dst + row * p.dst_nb0 + c * p.dst_nb1)
                        : dst_rope ? dst_rope
                                   : reinterpret_cast<float*>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + c * p.dst_nb1);
       if (row < p.n && l == 0) gstore<float>(o, acc[c]);
+    }
     }
     const int64_t gn = refill(s, true);
     if (s)
@@ -449,6 +484,17 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       g_0 = gn;
   }
   wait_vmem<0>();
+  if (M == 1 && p.swiglu_out) {
+    // the block: its 32 values in element order, quantised by 32 lanes
+    wg_barrier();
+    if (wv == 0 && lane < 32) {
+      float d;
+      const int q = q8_lane_quant(lds_load<float>(lds + kQ8SwVals + 4 * lane), d);
+      char* const blk = p.swiglu_out + 36 * (int64_t)blockIdx.x;
+      if (lane == 0) gstore<float>(blk, d);
+      gstore<signed char>(blk + 4 + lane, (signed char)q);
+    }
+  }
 }
 
 // The staged form, for rows longer than the ring's slots (e.g. a 4864-wide
@@ -583,6 +629,11 @@ hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+bool q8_swiglu_out_ok(const Q8MulMat& p, int n_cu) {
+  return p.swiglu_out && p.m == 1 && !p.add && !p.rope_on && !p.perm_hd && p.n % 64 == 0 &&
+         p.n / 64 <= (n_cu > 0 ? n_cu : 256) && q8_ring_form(p);
+}
+
 bool q8_ring_form(const Q8MulMat& p) {
   const bool act_ok = p.x ? (p.x_ld >= p.k && reinterpret_cast<uintptr_t>(p.x) % 4 == 0)
                           : (p.a_nb1 % 4 == 0 && reinterpret_cast<uintptr_t>(p.a) % 4 == 0);
@@ -616,7 +667,11 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) 
     }();
     if (attr != hipSuccess) return attr;
     const int64_t groups = (p.n + 7) / 8;
-    const unsigned grid = (unsigned)std::min<int64_t>(n_cu > 0 ? n_cu : 256, (groups + kQ8RingWaves - 1) / kQ8RingWaves);
+    if (p.swiglu_out && !q8_swiglu_out_ok(p, n_cu)) return hipErrorInvalidValue;
+    // with the SwiGLU epilogue one workgroup per 64-row block (8 groups)
+    const unsigned grid = p.swiglu_out ? (unsigned)(p.n / 64)
+                                       : (unsigned)std::min<int64_t>(n_cu > 0 ? n_cu : 256,
+                                                                     (groups + kQ8RingWaves - 1) / kQ8RingWaves);
     const bool epi = p.rope_on || p.perm_hd;
     hipLaunchKernelGGL(fns[epi ? 1 : 0][p.m - 1], dim3(grid), dim3(kQ8RingWaves * kWave), kQ8RingLdsAll, stream, p);
   } else if (q8_stage_lds_bytes(p.w_nb1, p.k) <= kQ8StageLdsMax &&

@@ -5,17 +5,19 @@
 // Device layout, allocated once at load:
 //   weights  one buffer; per layer the Q, K and V projection rows stacked into
 //            one [n_embd + 2 kv] x n_embd Q8_0 matrix (and their biases into
-//            one vector), gate and up stacked into one 2 n_ff x n_embd matrix,
-//            so a layer is 4 matrix launches; rows keep the GGUF block bytes
-//            (34-byte Q8_0 blocks), every matrix 256-byte aligned;
+//            one vector), gate and up rows interleaved into one 2 n_ff x n_embd
+//            matrix (row 2i gate_i, row 2i + 1 up_i), so a layer is 4 matrix
+//            launches; rows keep the GGUF block bytes (34-byte Q8_0 blocks),
+//            every matrix 256-byte aligned;
 //   KV       mi_hip_kv (F32, [head_dim, n_head_kv, n_ctx] per layer);
 //   acts     x [n_embd, T] (the residual stream), qkv [n_embd + 2 kv, T],
-//            attention output [head_dim, n_head, T], gate|up [2 n_ff, T],
+//            attention output [head_dim, n_head, T], gate/up pairs [2 n_ff, T],
 //            Q8_0 activation blocks for the widest input, logits [n_vocab, T].
 // Per layer: RMSNorm*w -> Q8_0 blocks (one kernel), QKV + bias (matrix
 // epilogue), RoPE + K/V append (one kernel), attention (decode or prefill
 // kernel), Q8_0 blocks of its output, O projection + residual (epilogue, in
-// place), RMSNorm*w -> blocks, gate|up, SiLU(gate)*up -> blocks (one kernel),
+// place), RMSNorm*w -> blocks, gate/up with SiLU(gate)*up -> blocks (the
+// matrix kernel's epilogue for one column, a kernel of its own for several),
 // down projection + residual. Then the final norm of the returned columns,
 // the lm_head and an argmax on the device.
 #include <hip/hip_runtime.h>
@@ -95,7 +97,8 @@ __global__ __launch_bounds__(kNormThreads) void norm_q8_kernel(const float* x, i
 }
 
 // SILU(gate) * up (src/ops_cpu.cpp:134-141, 167-170), quantised to Q8_0_ACT
-// blocks; one thread per element, 32 lanes to a block. silu(x) = x / (1 +
+// blocks from the interleaved gate/up pairs; one thread per element, 32 lanes
+// to a block. silu(x) = x / (1 +
 // expf(-x)) with the host C library's expf (libm_ref.h), so every value is the
 // engine's.
 __global__ void silu_mul_q8_kernel(const float* gu, int64_t gu_ld, int F, char* aq, int64_t aq_ld,
@@ -105,8 +108,8 @@ __global__ void silu_mul_q8_kernel(const float* gu, int64_t gu_ld, int F, char* 
   if (idx >= (int64_t)T * F) return;  // T * F % 32 == 0: whole 32-lane groups leave together
   const int64_t col = idx / F;
   const int e = (int)(idx - col * F);
-  const float g = gload<float>(gu + col * gu_ld + e);
-  const float y = (g / (1.0f + expf_ref(-g, kExpfTab))) * gload<float>(gu + col * gu_ld + F + e);
+  const float g = gload<float>(gu + col * gu_ld + 2 * e);
+  const float y = (g / (1.0f + expf_ref(-g, kExpfTab))) * gload<float>(gu + col * gu_ld + 2 * e + 1);
   float d;
   const int q = q8_lane_quant(y, d);
   char* blk = aq + col * aq_ld + 36 * (e / 32);
@@ -347,6 +350,21 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
     off = mi::align256(off + total);
     return start;
   };
+  // two matrices of rb-byte rows interleaved row by row (the first's row i
+  // at 2i, the second's at 2i + 1)
+  auto place_pair_rows = [&](const mi::GgufTensor* a, const mi::GgufTensor* b, size_t rb) {
+    const size_t rows = a->nbytes / rb;
+    std::vector<uint8_t> out(a->nbytes + b->nbytes);
+    for (size_t r = 0; r < rows; ++r) {
+      std::memcpy(out.data() + 2 * r * rb, a->data + r * rb, rb);
+      std::memcpy(out.data() + (2 * r + 1) * rb, b->data + r * rb, rb);
+    }
+    staged.push_back(std::move(out));
+    const size_t start = off;
+    pieces.push_back({staged.back().data(), staged.back().size(), off});
+    off = mi::align256(off + staged.back().size());
+    return start;
+  };
   const mi::GgufTensor *on, *ow = nullptr;
   int rc;
   if ((rc = check_tensor(f, "output_norm.weight", mi::kGgufTF32, E, 1, &on))) return rc;
@@ -378,7 +396,7 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
       return rc;
     lo[l] = {place({an}), place_rope_rows({wq, wk, wv}, E + m->kvd, (size_t)m->row_e),
              place_rope_rows({bq, bk, bv}, E + m->kvd, sizeof(float)),
-             place({wo}), place({fn}), place({wg, wu}), place({wd})};
+             place({wo}), place({fn}), place_pair_rows(wg, wu, (size_t)m->row_e), place({wd})};
   }
   // everything above is host-side validation; the device is touched from here on
   if ((rc = mi::rt_bind())) return rc;
@@ -466,9 +484,14 @@ int quantize_cols(const mi_hip_qwen2* m, const float* src, int64_t ne0, int64_t 
 // dst[:, j] (+)= W . act[:, j] for j < m_cols. Decode-sized calls take the
 // streaming matrix kernel with the norm / quantisation as its prologue (one
 // launch); the others run the norm or quantize kernel into m->aq first.
+// With swiglu_out (rows in gate/up pairs), one column is written as the
+// Q8_0_ACT blocks of SiLU(gate) * up at swiglu_out when the matrix kernel's
+// epilogue takes the shape (*swiglued says whether it did; otherwise dst holds
+// the pairs).
 int proj(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, int64_t k, Act act,
          int64_t m_cols, float* dst, int64_t dst_ld, const float* add, int64_t add_ld,
-         const mi::RopeEpi* rope = nullptr, bool* roped = nullptr) {
+         const mi::RopeEpi* rope = nullptr, bool* roped = nullptr, char* swiglu_out = nullptr,
+         bool* swiglued = nullptr) {
   mi::Q8MulMat p{};
   p.w = w;
   p.a = m->aq;
@@ -513,6 +536,11 @@ int proj(const mi_hip_qwen2* m, const char* w, int64_t row_bytes, int64_t n, int
     }
     if (roped) *roped = p.rope_on != 0;
   }
+  if (swiglu_out && m_cols == 1) {
+    p.swiglu_out = swiglu_out;
+    if (!mi::q8_swiglu_out_ok(p, mi::rt_n_cu())) p.swiglu_out = nullptr;
+  }
+  if (swiglued) *swiglued = p.swiglu_out != nullptr;
   hipError_t e = mi::launch_mul_mat_q8_0(p, mi::rt_n_cu(), m->stream);
   return e == hipSuccess ? MI_HIP_OK : mi::rt_hip_fail(e, "qwen2 mul_mat launch");
 }
@@ -646,13 +674,16 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
     }
     if (m->timing) Q2_TRY(hipEventRecord(m->ev[2 * l + 1], st), "hipEventRecord");
     if ((rc = proj(m, w.wo, m->row_e, E, E, {m->ao, nullptr}, T, m->x, E, m->x, E))) return rc;
+    bool swiglued = false;
     if ((rc = proj(m, w.wgu, m->row_e, 2 * (int64_t)F, E, {m->x, w.ffn_norm}, T, m->gu, 2 * (int64_t)F,
-                   nullptr, 0)))
+                   nullptr, 0, nullptr, nullptr, m->aq, &swiglued)))
       return rc;
-    const int64_t nel = (int64_t)T * F;
-    hipLaunchKernelGGL(mi::silu_mul_q8_kernel, dim3((unsigned)((nel + 255) / 256)), dim3(256), 0, st,
-                       m->gu, 2 * (int64_t)F, F, m->aq, ab_f, T);
-    Q2_TRY(hipGetLastError(), "silu launch");
+    if (!swiglued) {
+      const int64_t nel = (int64_t)T * F;
+      hipLaunchKernelGGL(mi::silu_mul_q8_kernel, dim3((unsigned)((nel + 255) / 256)), dim3(256), 0, st,
+                         m->gu, 2 * (int64_t)F, F, m->aq, ab_f, T);
+      Q2_TRY(hipGetLastError(), "silu launch");
+    }
     if ((rc = proj(m, w.wdown, m->row_f, E, F, {nullptr, nullptr}, T, m->x, E, m->x, E))) return rc;
   }
   const int first = last_only ? T - 1 : 0;

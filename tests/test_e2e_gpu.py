@@ -89,6 +89,22 @@ def test_greedy_ids_identical_to_reference(model05, e2e):
     assert ids == e2e["ids"], f"first difference at step {first_diff}"
 
 
+def test_one_token_step_equals_batched_bitwise(model05, e2e):
+    # reference-order mode: a one-token step (its FFN's SiLU(gate) * up formed
+    # in the down projection's prologue, its norms in the matrix kernels')
+    # against the last row of the batched prompt (separate SiLU, norm and
+    # quantize kernels) and against the reference engine's logits of that row
+    model05.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
+    prompt = e2e["prompt"]
+    want = np.load(os.path.join(GOLD, "e2e_qwen05_q8_0_logits.npz"))["logits_last"]
+    _, batched = model05.forward(prompt, n_past=0, want_logits=True)
+    model05.forward(prompt[:-1], n_past=0)
+    _, step = model05.forward(prompt[-1:], n_past=len(prompt) - 1, want_logits=True)
+    step = np.frombuffer(step, dtype=np.float32)
+    assert np.array_equal(bits(np.frombuffer(batched, dtype=np.float32)), bits(step))
+    assert np.array_equal(bits(step), bits(want))
+
+
 def test_fused_attention_end_to_end(model05, e2e):
     model05.set_attention(mh.MI_HIP_QWEN2_ATTN_FUSED)
     want = np.load(os.path.join(GOLD, "e2e_qwen05_q8_0_logits.npz"))["logits_last"]
