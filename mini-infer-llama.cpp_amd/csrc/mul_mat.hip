@@ -621,6 +621,107 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
   }
 }
 
+// The staged form for one column (a decode step's long rows, e.g. the FFN
+// down projection): kQ8S1Waves waves per 8-row group. The waves request the
+// group's rows and the column's blocks into LDS together; then each wave
+// forms the operands of one slice of the blocks -- float(int8 dot) and
+// fp16(w.d) * a.d per (block, lane), exactly the staged form's -- into LDS,
+// and wave 0 runs each lane's chain of multiply-adds over the blocks in order.
+// The same operations in the same order as the staged form, spread over the
+// workgroup: a single wave's operand work (5 LDS reads and ~12 vector
+// instructions per block) was the launch's longest phase.
+constexpr int kQ8S1Waves = 8;
+constexpr int kQ8S1LdsMax = 150 * 1024;
+
+// LDS of the one-column staged form: rows, the column's blocks (each region
+// whole 1 KB transfers), the operands.
+__host__ __device__ inline int64_t q8_s1_lds_bytes(int64_t w_nb1, int64_t k) {
+  return round1k(8 * w_nb1) + round1k(k / 32 * 36) + (k / 32) * kWave * 8;
+}
+
+__global__ __launch_bounds__(kQ8S1Waves * kWave) void mul_mat_q8_0_staged1_kernel(const Q8MulMat p) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char stage_lds[];
+  const lds_t* const lds = (const lds_t*)stage_lds;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int64_t g = blockIdx.x;
+  const int nrows = (int)min<int64_t>(8, p.n - g * 8);
+  const int64_t wbytes = (nrows - 1) * p.w_nb1 + p.k / 32 * 34;  // a multiple of 2
+  const char* const wsrc = p.w + g * 8 * p.w_nb1;
+  const int64_t wb4 = wbytes & ~int64_t(3);  // as in the staged form: a 2-byte tail is stored apart
+  const int nblk = (int)(p.k / 32);
+  const int abytes = nblk * 36;
+  const int64_t act_off = round1k(8 * p.w_nb1);
+  const int64_t op_off = act_off + round1k(abytes);
+  {
+    const rsrc_t r = make_rsrc(wsrc, (unsigned)wb4);
+    const int n1k = (int)((wbytes + 1023) / 1024);
+    for (int i = wv; i < n1k; i += kQ8S1Waves)
+      dma16(r, (lds_t*)stage_lds + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+    const rsrc_t ra = make_rsrc(p.a, (unsigned)abytes);  // q8_s1_ok: 16-byte aligned, whole 16-byte groups
+    for (int i = wv; i < (abytes + 1023) / 1024; i += kQ8S1Waves)
+      dma16(ra, (lds_t*)stage_lds + act_off + 1024 * i, (unsigned)(1024 * i + 16 * lane));
+  }
+  const int l = lane & 7, r = lane >> 3;
+  const int64_t row = g * 8 + r;
+  const bool live = r < nrows;
+  float addv = 0.0f;
+  if (wv == 0 && p.add) addv = gload<float>(p.add + min(row, p.n - 1) * p.add_nb0);
+  wait_vmem<0>();  // this wave's transfers (and the added term) have landed
+  wg_barrier();
+  if (wb4 != wbytes) {
+    if (threadIdx.x == 0) lds_store<unsigned short>((lds_t*)(stage_lds + wb4), gload<unsigned short>(wsrc + wb4));
+    wg_barrier();
+  }
+  // this wave's slice of the blocks: the operands of every (block, lane)
+  const lds_t* const w = lds + (live ? r : 0) * p.w_nb1;
+  const lds_t* const act = lds + act_off;
+  lds_t* const op = (lds_t*)stage_lds + op_off;
+  const int b_lo = nblk * wv / kQ8S1Waves, b_hi = nblk * (wv + 1) / kQ8S1Waves;
+  for (int b = b_lo; b < b_hi; ++b) {
+    const lds_t* wb = w + 34 * b;
+    const float wd = (float)__builtin_bit_cast(_Float16, lds_load<unsigned short>(wb));
+    const int wq = (int)((unsigned)lds_load<unsigned short>(wb + 2 + 4 * l) |
+                         ((unsigned)lds_load<unsigned short>(wb + 4 + 4 * l) << 16));
+    const float ad = lds_load<float>(act + 36 * b);
+    const int aq = lds_load<int>(act + 36 * b + 4 + 4 * l);
+    const f32x2_t o = {(float)__builtin_amdgcn_sdot4(wq, aq, 0, false), wd * ad};
+    lds_store<f32x2_t>(op + 8 * (b * kWave + lane), o);
+  }
+  wg_barrier();
+  if (wv != 0) return;
+  // the chain, 8 blocks' operands read ahead of their multiply-adds
+  float acc = 0.0f;
+  int b0 = 0;
+  for (; b0 + 8 <= nblk; b0 += 8) {
+    f32x2_t o[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o[u] = lds_load<f32x2_t>(op + 8 * ((b0 + u) * kWave + lane));
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(o[u].x, o[u].y, acc);
+  }
+  for (; b0 < nblk; ++b0) {
+    const f32x2_t o = lds_load<f32x2_t>(op + 8 * (b0 * kWave + lane));
+    acc = __builtin_fmaf(o.x, o.y, acc);
+  }
+  float s = acc + __shfl_xor(acc, 4, 8);
+  s = s + __shfl_xor(s, 1, 8);
+  s = s + __shfl_xor(s, 2, 8);
+  if (live && l == 0) {
+    if (p.add) s = s + addv;
+    gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0, s);
+  }
+}
+
+// One column through the staged form's workgroup-wide variant: whole 16-byte
+// groups of activation blocks at a 16-byte aligned address, and its LDS
+// within the budget.
+static bool q8_s1_ok(const Q8MulMat& p) {
+  return p.m == 1 && !p.x && !p.swiglu_out && (p.k / 32 * 36) % 16 == 0 && reinterpret_cast<uintptr_t>(p.a) % 16 == 0 &&
+         q8_s1_lds_bytes(p.w_nb1, p.k) <= kQ8S1LdsMax;
+}
+
 hipError_t launch_quantize_q8_0_act(const Q8Quantize& p, hipStream_t stream) {
   const int64_t n = p.rows * (p.ne0 / 32);
   if (n == 0) return hipSuccess;
@@ -687,6 +788,14 @@ hipError_t launch_mul_mat_q8_0(const Q8MulMat& p, int n_cu, hipStream_t stream) 
     }();
     if (attr != hipSuccess) return attr;
     const dim3 grid((unsigned)((p.n + 7) / 8));
+    if (q8_s1_ok(p)) {
+      static const hipError_t attr1 = hipFuncSetAttribute((const void*)&mul_mat_q8_0_staged1_kernel,
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize, kQ8S1LdsMax);
+      if (attr1 != hipSuccess) return attr1;
+      hipLaunchKernelGGL(mul_mat_q8_0_staged1_kernel, grid, dim3(kQ8S1Waves * kWave),
+                         (unsigned)q8_s1_lds_bytes(p.w_nb1, p.k), stream, p);
+      return hipGetLastError();
+    }
     const unsigned lds = (unsigned)q8_stage_lds_bytes(p.w_nb1, p.k);
     if (p.m == 1)
       hipLaunchKernelGGL(mul_mat_q8_0_staged_kernel<1>, grid, dim3(kWave), lds, stream, p);
