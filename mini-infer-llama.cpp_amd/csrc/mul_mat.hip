@@ -262,11 +262,15 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     for (int i = t; i < (kQ8MaxBlocks - nblk) * 9; i += kT)
       *reinterpret_cast<unsigned*>(act_lds + abytes + 4 * i) = 0u;
     wg_barrier();  // the counter is zero (the loads above stay in flight)
-    // both slots are requested even for an empty take: the compiler then
-    // knows that exactly 16 requests follow the loads above, and waits for
-    // those loads with vmcnt(16)
+    // slot 0 is requested even for an empty take, so that exactly 8
+    // requests follow the loads above: the compiler's wait for them (at the
+    // empty asm, which reads them all) is vmcnt(8). Then slot 1, with no
+    // requests for an empty take (a wave with one group has nothing to issue
+    // there): its count is known only at run time, and the loads above are
+    // no longer waited for after it.
     g_0 = refill(0, true);
-    g_1 = refill(1, true);
+    asm volatile("" ::"v"(xv[0]), "v"(xv[1]), "v"(nw[0]), "v"(nw[1]), "v"(av), "v"(te));
+    g_1 = refill(1, false);
     if (!p.x) {
       if (t < abytes / 4) *reinterpret_cast<unsigned*>(act_lds + 4 * t) = av;
     } else {
@@ -353,6 +357,7 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
   }
   // slots in turn until the first empty one (a wave's takes increase, so
   // every later slot is empty too)
+  const bool one_slot = M == 1 && g_1 < 0;  // the first fill issued slot 0's requests only
   for (int s = 0, it = 0;; s ^= 1, ++it) {
     const int64_t g = s ? g_1 : g_0;
     if (g < 0) break;
@@ -380,7 +385,9 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       }
     }
     // (the SwiGLU epilogue issues no stores: it writes LDS)
-    if (it == 0)
+    if (it == 0 && one_slot)
+      wait_vmem_plus<0>(extra);
+    else if (it == 0)
       wait_vmem_plus<8>(extra);
     else if (M == 1 && p.swiglu_out)
       wait_vmem_plus<8>(extra);
