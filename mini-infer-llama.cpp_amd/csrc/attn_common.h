@@ -315,18 +315,103 @@ __device__ __forceinline__ void chunks(unsigned sq, f32x4_t (&b)[3][4], float& s
     chunks<C + 1, KC>(sq, b, s);
   }
 }
+// s plus the N floats at LDS byte address sq, one rounded addition each, in order
+template <int N>
+__device__ __forceinline__ float run(unsigned sq, float s) {
+  static_assert(N % 16 == 0 && 4 * N <= 65536, "whole chunks of 16, offsets in range");
+  f32x4_t b[3][4];
+  load<0>(sq, b[0]);
+  if constexpr (N / 16 > 1) load<1>(sq, b[1]);
+  chunks<0, N / 16>(sq, b, s);
+  return s;
+}
 }  // namespace sum_lds
 
 template <int N>
 __device__ __forceinline__ float ordered_sum_lds(const lds_t* sq) {
-  static_assert(N % 16 == 0 && N >= 32 && 4 * N <= 65536, "whole chunks of 16, offsets in range");
-  const unsigned a = (unsigned)(uintptr_t)sq;
-  sum_lds::f32x4_t b[3][4];
-  sum_lds::load<0>(a, b[0]);
-  sum_lds::load<1>(a, b[1]);
-  float s = 0.0f;
-  sum_lds::chunks<0, N / 16>(a, b, s);
-  return s;
+  return sum_lds::run<N>((unsigned)(uintptr_t)sq, 0.0f);
+}
+
+// The same ordered sum of 8 * L non-negative floats at sq (LDS; callers pad
+// with +0.0), formed by 8 waves together, every wave returning it. Segment j
+// (floats jL .. jL + L - 1) belongs to wave j, which runs the segment's chain
+// of additions from 64 start values at once, one per lane: the consecutive
+// floats from 32 below g_j, the float nearest to the exact sum of the floats
+// before the segment (a sum in double: it only places the candidates). The
+// true start of segment j is the end of segment j - 1's chain from its own
+// true start, so each wave then walks the segments in order, taking for each
+// the lane whose start equals the running sum (non-negative floats are
+// ordered like their bit patterns, so that lane is the bit difference), or,
+// if the running sum is not among the 64 (a rounding drift of more than 32
+// ulps from the exact prefix), continuing the chain itself. The result is
+// the one-lane sum's to the bit, in about a quarter of its time. work: 8 * 8
+// + 8 * 64 * 4 bytes of LDS, 16-byte aligned. Every wave of the workgroup
+// calls it (two barriers).
+// The walk's way out when a running sum is not among a segment's candidates
+// (kept out of line: it is rare).
+template <int L>
+__device__ __noinline__ float ordered_sum_continue(unsigned sq, float s) {
+  return sum_lds::run<L>(sq, s);
+}
+
+template <int L>
+__device__ float ordered_sum_lds_8waves(const lds_t* sq, lds_t* work, int wv, int lane) {
+#pragma clang fp contract(off)
+  static_assert(L % 16 == 0 && L <= 2 * kWave, "whole chunks of 16, at most two floats per lane");
+  typedef double f64x2_t __attribute__((ext_vector_type(2)));
+  const unsigned a_sq = (unsigned)(uintptr_t)sq;
+  const unsigned a_q = (unsigned)(uintptr_t)work;  // 8 segment sums (double)
+  const unsigned a_r = a_q + 64;                   // 8 x 64 chain ends
+  const unsigned seg = a_sq + 4 * L * wv;
+  // (LDS reads as asm: the compiler cannot tell these runtime addresses from
+  // LDS-direct requests in flight elsewhere, and would wait for those)
+  float v0 = 0.0f, v1 = 0.0f;
+  asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:256\n\ts_waitcnt lgkmcnt(0)"
+               : "=&v"(v0), "=&v"(v1) : "v"(seg + 4 * lane));
+  double q = (lane < L ? (double)v0 : 0.0) + (lane + kWave < L ? (double)v1 : 0.0);
+#pragma unroll
+  for (int m = kWave / 2; m > 0; m >>= 1) q += __shfl_xor(q, m);
+  if (lane == 0) lds_store<double>(work + 8 * wv, q);
+  wg_barrier();
+  f64x2_t q01, q23, q45, q67;  // work is 16-byte aligned
+  asm volatile(
+      "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:16\n\t"
+      "ds_read_b128 %2, %4 offset:32\n\tds_read_b128 %3, %4 offset:48\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(q01), "=&v"(q23), "=&v"(q45), "=&v"(q67)
+      : "v"(a_q));
+  const double qs[8] = {q01.x, q01.y, q23.x, q23.y, q45.x, q45.y, q67.x, q67.y};
+  // every segment's lowest candidate (the same on every wave)
+  int base[8];
+  double pre = 0.0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int gb = __builtin_bit_cast(int, (float)pre);
+    base[j] = gb > 32 ? gb - 32 : 0;
+    pre += qs[j];
+  }
+  int my_base = base[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) my_base = wv == j ? base[j] : my_base;
+  const float end = sum_lds::run<L>(seg, __builtin_bit_cast(float, my_base + lane));
+  lds_store<float>(work + 64 + 4 * (kWave * wv + lane), end);
+  wg_barrier();
+  float e[8];
+  asm volatile(
+      "ds_read_b32 %0, %8\n\tds_read_b32 %1, %8 offset:256\n\tds_read_b32 %2, %8 offset:512\n\t"
+      "ds_read_b32 %3, %8 offset:768\n\tds_read_b32 %4, %8 offset:1024\n\tds_read_b32 %5, %8 offset:1280\n\t"
+      "ds_read_b32 %6, %8 offset:1536\n\tds_read_b32 %7, %8 offset:1792\n\ts_waitcnt lgkmcnt(0)"
+      : "=&v"(e[0]), "=&v"(e[1]), "=&v"(e[2]), "=&v"(e[3]), "=&v"(e[4]), "=&v"(e[5]), "=&v"(e[6]), "=&v"(e[7])
+      : "v"(a_r + 4 * lane));
+  float tot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int c = __builtin_bit_cast(int, tot) - base[j];
+    if (c >= 0 && c < kWave)
+      tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e[j]), c));
+    else
+      tot = ordered_sum_continue<L>(a_sq + 4 * L * j, tot);
+  }
+  return tot;
 }
 
 // One Q8_0_ACT block from 32 lanes (an aligned group of 32 lanes, each holding

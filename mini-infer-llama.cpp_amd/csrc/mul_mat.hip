@@ -143,8 +143,10 @@ constexpr int kQ8ActBytesMax = kQ8Cols * kQ8MaxBlocks * 36;
 constexpr int kQ8RingTake = kQ8RingWaves * 2 * kQ8Slot + kQ8ActBytesMax;  // the group counter
 constexpr int kQ8Scale = kQ8RingTake + 16;        // the norm scale of each column
 constexpr int kQ8RingLds = kQ8Scale + 4 * kQ8Cols;
-constexpr int kQ8XOff = kQ8RingLds;                // one F32 column (M = 1), past the ring
-constexpr int kQ8SwTab = kQ8XOff + kQ8MaxBlocks * 32 * 4;  // SwiGLU epilogue: expf's table
+constexpr int kQ8XOff = kQ8RingLds;                // one F32 column's squares (M = 1), past the ring,
+constexpr int kQ8SqN = 8 * 128;                    // padded to the 8 waves' segments of 128
+constexpr int kQ8SumWork = kQ8XOff + 4 * kQ8SqN;   // the 8-wave ordered sum's work area
+constexpr int kQ8SwTab = kQ8SumWork + 64 + 8 * kWave * 4;  // SwiGLU epilogue: expf's table
 constexpr int kQ8SwVals = kQ8SwTab + 32 * 8;                 // and the workgroup's 32 values
 constexpr int kQ8RingLdsAll = kQ8SwVals + 32 * 4;
 
@@ -276,15 +278,14 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     } else {
       float scale = 1.0f;
       if (p.norm_w) {
-        // the squares, padded with +0.0 to kQ8MaxBlocks * 32
+        // the squares, padded with +0.0 to kQ8SqN; their sum in the
+        // reference's order, formed by the 8 waves together
+        static_assert(kQ8RingWaves == 8 && 2 * kT == kQ8SqN, "8 waves, two squares per thread");
         lds_t* const sq = lds + kQ8XOff;
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          if (t + kT * j < kQ8MaxBlocks * 32) lds_store<float>(sq + 4 * (t + kT * j), t + kT * j < k ? xv[j] * xv[j] : 0.0f);
+        for (int j = 0; j < 2; ++j) lds_store<float>(sq + 4 * (t + kT * j), t + kT * j < k ? xv[j] * xv[j] : 0.0f);
         wg_barrier();
-        if (t == 0) lds_store<float>(s_scale, rms_scale(ordered_sum_lds<kQ8MaxBlocks * 32>(sq), k, p.eps));
-        wg_barrier();
-        scale = lds_load<float>(s_scale);
+        scale = rms_scale(ordered_sum_lds_8waves<kQ8SqN / 8>(sq, lds + kQ8SumWork, wv, lane), k, p.eps);
       }
       // one thread per element in groups of 32 lanes forming each block (k
       // and kT are multiples of 32, so a group is active as a whole)

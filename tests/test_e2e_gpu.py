@@ -220,6 +220,33 @@ def test_tiny_incremental_prefill_equals_batched_bitwise(tiny):
                               bits(np.frombuffer(step, dtype=np.float32)))
 
 
+def test_norm_sum_walk_way_out_bitwise(tmp_path):
+    # A token whose embedding row is 256 equal values (3.7): the squares' sum
+    # in the reference's order rounds the same way at every step and drifts
+    # more than 32 ulps from the exact prefix sums, so the 8-wave ordered sum
+    # of the one-token steps' norm leaves its 64 candidates and continues the
+    # chain itself (a float32 emulation of the walk takes that way out for 6
+    # of the 8 segments of this row). The one-token steps must still equal the
+    # batched prompt, whose norm is one lane's serial sum, bit for bit.
+    seed, tok, val = 21, 5, 3.7
+    path = str(tmp_path / "const_row.gguf")
+    gg.write_qwen2_q8_0(path, seed, dict(TINY, embd_type=gg.T_F32))
+    data = bytearray(open(path, "rb").read())
+    start = bytes(data).index(gg.normal_chunk(seed, 0, 0, 4).tobytes())  # token_embd's first floats
+    E = TINY["n_embd"]
+    data[start + 4 * tok * E:start + 4 * (tok + 1) * E] = np.full(E, val, dtype=np.float32).tobytes()
+    with open(path, "wb") as f:
+        f.write(bytes(data))
+    prompt = [tok, 17, tok, 3]
+    with Qwen2(path, n_ctx=64, max_tokens=len(prompt)) as m:
+        m.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
+        _, batched = m.forward(prompt, n_past=0, want_logits=True)
+        for i, t in enumerate(prompt):
+            _, step = m.forward([t], n_past=i, want_logits=True)
+        assert np.array_equal(bits(np.frombuffer(batched, dtype=np.float32)),
+                              bits(np.frombuffer(step, dtype=np.float32)))
+
+
 @pytest.mark.parametrize("embd_type", [gg.T_F16, gg.T_F32])
 def test_tiny_model_unquantised_embedding_with_separate_lm_head(tmp_path, embd_type):
     # token_embd in F16 / F32 (the embedding lookup's other types) and a separate
