@@ -182,8 +182,9 @@ __device__ inline float wave_sum(float x) {
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // DPP lane moves (VALU, no LDS). Within each row of 16 lanes:
-//   xor1 / xor2: quad_perm [1,0,3,2] / [2,3,0,1]; half_mirror: i <-> 7-i;
-//   mirror: i <-> 15-i; bcast<J>: lane J of the row to the whole row.
+//   xor1 / xor2: quad_perm [1,0,3,2] / [2,3,0,1] (0xB1 / 0x4E); half_mirror:
+//   i <-> 7-i; mirror: i <-> 15-i; row_ror:N (0x120 + N): lane i takes lane
+//   (i + N) % 16; bcast<J>: lane J of the row to the whole row.
 template <int CTRL>
 __device__ inline float dpp_mov(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
@@ -347,6 +348,30 @@ __device__ __forceinline__ float ordered_sum_lds(const lds_t* sq) {
 // the one-lane sum's to the bit, in about a quarter of its time. work: 8 * 8
 // + 8 * 64 * 4 bytes of LDS, 16-byte aligned. Every wave of the workgroup
 // calls it (two barriers).
+// A wave's sum of one double per lane, on every lane, without the LDS pipe:
+// quad and row rotations by DPP moves, then the four row sums by readlane
+// (a fixed order, so every lane and every call gets the same bits).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const unsigned lo = __builtin_bit_cast(unsigned, dpp_mov<CTRL>(__builtin_bit_cast(float, (unsigned)b)));
+  const unsigned hi = __builtin_bit_cast(unsigned, dpp_mov<CTRL>(__builtin_bit_cast(float, (unsigned)(b >> 32))));
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum_f64(double x) {
+  x += dpp_f64<0xB1>(x);   // quad_perm [1,0,3,2]
+  x += dpp_f64<0x4E>(x);   // quad_perm [2,3,0,1]: every lane holds its quad's sum
+  x += dpp_f64<0x124>(x);  // row_ror:4
+  x += dpp_f64<0x128>(x);  // row_ror:8: every lane holds its row's sum
+  auto lane_val = [&](int l) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+  };
+  return ((lane_val(0) + lane_val(16)) + lane_val(32)) + lane_val(48);
+}
+
 // The walk's way out when a running sum is not among a segment's candidates
 // (kept out of line: it is rare).
 template <int L>
@@ -368,9 +393,7 @@ __device__ float ordered_sum_lds_8waves(const lds_t* sq, lds_t* work, int wv, in
   float v0 = 0.0f, v1 = 0.0f;
   asm volatile("ds_read_b32 %0, %2\n\tds_read_b32 %1, %2 offset:256\n\ts_waitcnt lgkmcnt(0)"
                : "=&v"(v0), "=&v"(v1) : "v"(seg + 4 * lane));
-  double q = (lane < L ? (double)v0 : 0.0) + (lane + kWave < L ? (double)v1 : 0.0);
-#pragma unroll
-  for (int m = kWave / 2; m > 0; m >>= 1) q += __shfl_xor(q, m);
+  const double q = wave_sum_f64((lane < L ? (double)v0 : 0.0) + (lane + kWave < L ? (double)v1 : 0.0));
   if (lane == 0) lds_store<double>(work + 8 * wv, q);
   wg_barrier();
   f64x2_t q01, q23, q45, q67;  // work is 16-byte aligned
@@ -417,14 +440,24 @@ __device__ float ordered_sum_lds_8waves(const lds_t* sq, lds_t* work, int wv, in
 // One Q8_0_ACT block from 32 lanes (an aligned group of 32 lanes, each holding
 // element lane % 32): returns this lane's int8 and, in d, the block scale
 // (amax / 127), as the engine's row quantiser.
+// The group's amax: within each 16-lane row by DPP moves (quad swaps, row
+// rotations), then across the group's two rows by one lane exchange; a max
+// does not depend on the order (a lane whose own value is NaN keeps NaN, as
+// with any order of strict greater-than steps). The whole group is active or
+// inactive together.
 __device__ inline int q8_lane_quant(float y, float& d) {
 #pragma clang fp contract(off)
   float amax = fabsf(y);
-#pragma unroll
-  for (int m = 16; m > 0; m >>= 1) {
-    const float o = __shfl_xor(amax, m, 32);
-    amax = o > amax ? o : amax;
-  }
+  float o = dpp_mov<0xB1>(amax);  // quad_perm [1,0,3,2]
+  amax = o > amax ? o : amax;
+  o = dpp_mov<0x4E>(amax);  // quad_perm [2,3,0,1]
+  amax = o > amax ? o : amax;
+  o = dpp_mov<0x124>(amax);  // row_ror:4
+  amax = o > amax ? o : amax;
+  o = dpp_mov<0x128>(amax);  // row_ror:8
+  amax = o > amax ? o : amax;
+  o = __shfl_xor(amax, 16, 32);
+  amax = o > amax ? o : amax;
   d = amax / 127.0f;
   const float id = d != 0.0f ? 1.0f / d : 0.0f;
   int q = (int)__builtin_rintf(y * id);
