@@ -40,6 +40,22 @@ __device__ inline float swiglu_value(float g, float u, Tab tab) {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
+// The horizontal sum of an 8-lane row group's accumulators in the order of the
+// reference's AVX2 reduction, ((a0 + a4) + (a1 + a5)) + ((a2 + a6) + (a3 + a7)),
+// on every lane of the group (float addition is commutative, so both lanes of
+// a pair form the same value). The partners come by DPP moves, not the LDS
+// pipe: lane l ^ 4 by a row shift (left for l & 4 == 0, right otherwise), then
+// quad swaps for l ^ 1 and l ^ 2.
+__device__ inline float q8_hsum8(float a, int lane) {
+#pragma clang fp contract(off)
+  const float up = dpp_mov<0x104>(a), down = dpp_mov<0x114>(a);  // row_shl:4, row_shr:4
+  float t = a + ((lane & 4) ? down : up);
+  t = t + dpp_mov<0xB1>(t);  // quad_perm [1,0,3,2]
+  return t + dpp_mov<0x4E>(t);  // quad_perm [2,3,0,1]
+}
+// Row group rs ^ 1's value (8 lanes away): a row rotation by 8.
+__device__ inline float q8_xor8(float a) { return dpp_mov<0x128>(a); }
+
 // One thread per 32-element block of one activation row.
 __global__ void quantize_q8_0_act_kernel(const Q8Quantize p) {
 #pragma clang fp contract(off)
@@ -113,9 +129,7 @@ __global__ __launch_bounds__(256) void mul_mat_q8_0_kernel(const Q8MulMat p) {
       if (c < nc) {
         // lanes l and l^4 -> acc_l + acc_(l+4); then pairs; lane 0 holds
         // ((acc0 + acc4) + (acc1 + acc5)) + ((acc2 + acc6) + (acc3 + acc7))
-        float s = acc[c] + __shfl_xor(acc[c], 4, 8);
-        s = s + __shfl_xor(s, 1, 8);
-        s = s + __shfl_xor(s, 2, 8);
+        float s = q8_hsum8(acc[c], threadIdx.x);
         if (live && l == 0) {
           if (p.add) s = s + gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1);
           gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
@@ -426,9 +440,7 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     }
 #pragma unroll
     for (int c = 0; c < M; ++c) {
-      float t = acc[c] + __shfl_xor(acc[c], 4, 8);
-      t = t + __shfl_xor(t, 1, 8);
-      t = t + __shfl_xor(t, 2, 8);
+      const float t = q8_hsum8(acc[c], lane);
       acc[c] = t;
     }
     // the added term's loads finish (vmcnt 0, which also drains the other
@@ -448,7 +460,7 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
     if constexpr (EPI && M == 1) {
       if (p.rope_on) {
         const RopeEpi& re = p.rope;
-        const float other = __shfl_xor(acc[0], 8);
+        const float other = q8_xor8(acc[0]);
         const int64_t qk_rows = (int64_t)re.n_q + re.n_kv;
         const int64_t h = row / re.hd;  // head (Q heads, then K heads, then V heads)
         const int w = (int)(row - h * re.hd);
@@ -472,7 +484,7 @@ __global__ __launch_bounds__(kQ8RingWaves * kWave) void mul_mat_q8_0_ring_kernel
       // gate rows are even, their up rows 8 lanes away: the group's 4 values
       // go to the workgroup's block in LDS (the workgroup's groups are the
       // block's 8)
-      const float up = __shfl_xor(acc[0], 8);
+      const float up = q8_xor8(acc[0]);
       if ((rs & 1) == 0 && l == 0)
         lds_store<float>(lds + kQ8SwVals + 4 * (4 * (int)(g - glo) + (rs >> 1)),
                          swiglu_value(acc[0], up, (const __attribute__((address_space(3))) uint64_t*)(lds + kQ8SwTab)));
@@ -617,9 +629,7 @@ __global__ __launch_bounds__(kWave) void mul_mat_q8_0_staged_kernel(const Q8MulM
 #pragma unroll
     for (int c = 0; c < MC; ++c) {
       if (MC == 1 || c < nc) {
-        float s = acc[c] + __shfl_xor(acc[c], 4, 8);
-        s = s + __shfl_xor(s, 1, 8);
-        s = s + __shfl_xor(s, 2, 8);
+        float s = q8_hsum8(acc[c], threadIdx.x);
         if (live && l == 0) {
           if (p.add) s = s + (MC == 1 ? addv : gload<float>(p.add + row * p.add_nb0 + (c0 + c) * p.add_nb1));
           gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0 + (c0 + c) * p.dst_nb1, s);
@@ -713,9 +723,7 @@ __global__ __launch_bounds__(kQ8S1Waves * kWave) void mul_mat_q8_0_staged1_kerne
     const f32x2_t o = lds_load<f32x2_t>(op + 8 * (b0 * kWave + lane));
     acc = __builtin_fmaf(o.x, o.y, acc);
   }
-  float s = acc + __shfl_xor(acc, 4, 8);
-  s = s + __shfl_xor(s, 1, 8);
-  s = s + __shfl_xor(s, 2, 8);
+  float s = q8_hsum8(acc, lane);
   if (live && l == 0) {
     if (p.add) s = s + addv;
     gstore<float>(p.dst + q8_unperm_row(row, p.perm_hd, p.perm_rows) * p.dst_nb0, s);
