@@ -9,12 +9,17 @@
 //   P_i  = e_i * (1 / sum)
 //   O[o] = sum_t V[o, kvh, t] * P_t            t ascending (masked t add +-0, skipped)
 //
-// One wave per (token j, head h): lanes split the keys for the scores and the
-// exponentials, lane 0 runs the ordered sum, and lanes split the output
-// elements for the ordered V sums. The ordered sums make a row's cost linear
-// in its key count on one lane: this is the checking path for whole-model
-// parity (token ids equal to the reference engine's), not the throughput path
-// (decode.hip / prefill.hip).
+// Rows whose keys' V fit in LDS (a * head_dim * 4 <= kExactStageBytes) run
+// attn_exact_staged_kernel: 256 threads per (token j, head h); the row's V
+// rows are requested into LDS (LDS-direct, 16 bytes per lane) at the start and
+// land while the threads form one key's score each, the maximum, and the
+// exponentials; lane 0 runs the ordered sum; then each output element's lane
+// runs its ordered V sum from LDS. Longer rows run attn_exact_kernel: one wave
+// per (token, head), lanes splitting the keys and then the output elements,
+// V read from global memory. Either way the ordered sums make a row's cost
+// linear in its key count on one lane: this is the checking path for
+// whole-model parity (token ids equal to the reference engine's), not the
+// throughput path (decode.hip / prefill.hip).
 #include <cmath>
 
 #include "attn_common.h"
@@ -79,8 +84,120 @@ __global__ __launch_bounds__(kWave) void attn_exact_kernel(const ExactAttn p) {
   }
 }
 
+constexpr int kExactStageBytes = 128 * 1024;  // the staged kernel's V rows
+constexpr int kExactThreads = 256;
+
+// LDS of the staged kernel for rows of up to n_kv keys: the V rows (whole 1 KB
+// transfers), the probabilities, expf's table, the wave maxima and 1 / sum.
+__host__ __device__ inline int exact_staged_lds(int n_kv, int d) {
+  return ((n_kv * d * 4 + 1023) & ~1023) + 4 * n_kv + 32 * 8 + 4 * 4 + 16;
+}
+
+// D: head_dim (64 or 128), so that a key's row loads are all issued at once.
+template <int D>
+__global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const ExactAttn p) {
+#pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) char ex_lds[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int h = blockIdx.x % p.n_head;
+  const int j = blockIdx.x / p.n_head;
+  const int kvh = h / p.n_rep;
+  const int a = min(p.n_past + j + 1, p.n_past + p.n_tokens);
+  const int n_kv = p.n_past + p.n_tokens;
+  const int vbytes = (n_kv * D * 4 + 1023) & ~1023;
+  float* const vl = reinterpret_cast<float*>(ex_lds);  // V row t at vl + t D
+  float* const prob = reinterpret_cast<float*>(ex_lds + vbytes);
+  uint64_t* const tab = reinterpret_cast<uint64_t*>(ex_lds + vbytes + 4 * n_kv);
+  float* const red = reinterpret_cast<float*>(tab + 32);
+  const uint64_t te = kExpfTab[lane & 31];  // requested first: loads complete in order
+  // the row's V rows into LDS: piece i (16 bytes) is row i / (D / 4), bytes
+  // 16 (i % (D / 4)); pieces past the row arrive as zeros. The keys' loads
+  // below complete behind these requests (in order), so V has landed before
+  // the scores are formed, and nothing after them waits on memory.
+  {
+    const char* const vbase = p.v + kvh * p.v_s1;
+    const unsigned vsize = (unsigned)((int64_t)(a - 1) * p.v_s2 + 4 * D);
+    const rsrc_t r = make_rsrc(vbase, vsize);
+    const int pieces = a * D / 4, ppr = D / 4;
+    for (int i0 = kWave * wv; i0 < pieces; i0 += kExactThreads) {
+      const int i = i0 + lane;
+      const unsigned off = i < pieces ? (unsigned)((int64_t)(i / ppr) * p.v_s2 + 16 * (i % ppr)) : vsize;
+      dma16(r, (lds_t*)ex_lds + 16 * i0, off);
+    }
+  }
+  // one key's score per thread, d ascending, product and sum each rounded
+  const float* q = reinterpret_cast<const float*>(p.q + h * p.q_s1 + (int64_t)j * p.q_s2);
+  float mx = -INFINITY;
+  for (int i = tid; i < a; i += kExactThreads) {
+    const float* kr = reinterpret_cast<const float*>(p.k + kvh * p.k_s1 + (int64_t)i * p.k_s2);
+    float4 kv[D / 4];
+#pragma unroll
+    for (int u = 0; u < D / 4; ++u) kv[u] = *reinterpret_cast<const float4*>(kr + 4 * u);
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < D / 4; ++u) {
+      const float4 qv = *reinterpret_cast<const float4*>(q + 4 * u);
+      acc = acc + kv[u].x * qv.x;
+      acc = acc + kv[u].y * qv.y;
+      acc = acc + kv[u].z * qv.z;
+      acc = acc + kv[u].w * qv.w;
+    }
+    const float v = acc * p.scale;
+    prob[i] = v;
+    mx = v > mx ? v : mx;
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    const float o = __shfl_xor(mx, off);
+    mx = o > mx ? o : mx;
+  }
+  if (tid < 32) tab[tid] = te;
+  if (lane == 0) red[wv] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int w = 1; w < kExactThreads / kWave; ++w) mx = red[w] > mx ? red[w] : mx;
+  for (int i = tid; i < a; i += kExactThreads) prob[i] = expf_ref(prob[i] - mx, tab);
+  __syncthreads();
+  if (tid == 0) {
+    float sum = 0.0f;
+    for (int i = 0; i < a; ++i) sum = sum + prob[i];
+    red[4] = (float)(1.0 / (double)sum);  // the correctly rounded 1.0f / sum
+  }
+  __syncthreads();
+  const float inv = red[4];
+  for (int i = tid; i < a; i += kExactThreads) prob[i] = prob[i] * inv;
+  wait_vmem<0>();  // this wave's V requests have landed
+  __syncthreads();
+  if (tid < D) {
+    float acc = 0.0f;
+    for (int t = 0; t < a; ++t) acc = acc + vl[t * D + tid] * prob[t];
+    float* out = reinterpret_cast<float*>(p.out + h * p.o_s1 + (int64_t)j * p.o_s2);
+    out[tid] = acc;
+  }
+}
+
 hipError_t launch_attn_exact(const ExactAttn& p, hipStream_t stream) {
   const int n_kv = p.n_past + p.n_tokens;
+  if ((int64_t)n_kv * p.head_dim * 4 <= kExactStageBytes && (p.head_dim == 64 || p.head_dim == 128) &&
+      p.v_s2 % 4 == 0 && reinterpret_cast<uintptr_t>(p.v) % 4 == 0 && p.v_s1 % 4 == 0) {
+    static const hipError_t attr = [] {
+      hipError_t e = hipFuncSetAttribute((const void*)&attn_exact_staged_kernel<64>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         exact_staged_lds(kExactStageBytes / (4 * 64), 64));
+      if (e == hipSuccess)
+        e = hipFuncSetAttribute((const void*)&attn_exact_staged_kernel<128>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                exact_staged_lds(kExactStageBytes / (4 * 128), 128));
+      return e;
+    }();
+    if (attr != hipSuccess) return attr;
+    const dim3 grid((unsigned)(p.n_tokens * p.n_head));
+    const size_t lds = (size_t)exact_staged_lds(n_kv, p.head_dim);
+    if (p.head_dim == 64)
+      hipLaunchKernelGGL(attn_exact_staged_kernel<64>, grid, dim3(kExactThreads), lds, stream, p);
+    else
+      hipLaunchKernelGGL(attn_exact_staged_kernel<128>, grid, dim3(kExactThreads), lds, stream, p);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)n_kv * sizeof(float);
   static const hipError_t attr = hipFuncSetAttribute(
       (const void*)&attn_exact_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kExactMaxKeys * 4);
