@@ -47,6 +47,7 @@ __global__ __launch_bounds__(kWave) void attn_exact_kernel(const ExactAttn p) {
   for (int i = lane; i < a; i += kWave) {
     const float* kr = reinterpret_cast<const float*>(p.k + kvh * p.k_s1 + (int64_t)i * p.k_s2);
     float acc = 0.0f;
+#pragma unroll 16  // (the row's loads in flight together)
     for (int d = 0; d < D; d += 4) {
       const float4 kv = *reinterpret_cast<const float4*>(kr + d);
       const float4 qv = *reinterpret_cast<const float4*>(q + d);
@@ -78,6 +79,7 @@ __global__ __launch_bounds__(kWave) void attn_exact_kernel(const ExactAttn p) {
   const char* vbase = p.v + kvh * p.v_s1;
   for (int o = lane; o < D; o += kWave) {
     float acc = 0.0f;
+#pragma unroll 16  // (16 keys' loads in flight ahead of the ordered additions)
     for (int t = 0; t < a; ++t)
       acc = acc + *reinterpret_cast<const float*>(vbase + (int64_t)t * p.v_s2 + 4 * o) * prob[t];
     out[o] = acc;

@@ -50,7 +50,11 @@ def case_inputs(c):
 
 @pytest.fixture(scope="session")
 def hip():
-    """The HIP library, initialised on device 0. Only for tests marked gpu."""
+    """The HIP library, initialised on device 0. Only for tests marked gpu.
+    Every GPU test module requests it (directly or through usefixtures), so
+    that torch's HIP runtime initialises the device before the library's own
+    does: with the order reversed, torch.cuda.is_available() has reported no
+    device in the same process."""
     import torch
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")

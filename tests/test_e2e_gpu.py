@@ -34,7 +34,7 @@ import mi_hip_attn as mh
 import qwen2_gguf as gg
 from qwen2 import Qwen2
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip")]  # torch initialises the device first
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 GOLD = os.path.join(ROOT, "tests", "golden")
@@ -91,7 +91,7 @@ def test_greedy_ids_identical_to_reference(model05, e2e):
 
 def test_one_token_step_equals_batched_bitwise(model05, e2e):
     # reference-order mode: a one-token step (its FFN's SiLU(gate) * up formed
-    # in the down projection's prologue, its norms in the matrix kernels')
+    # in the gate/up matrix kernel's epilogue, its norms in the matrix kernels')
     # against the last row of the batched prompt (separate SiLU, norm and
     # quantize kernels) and against the reference engine's logits of that row
     model05.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
@@ -218,6 +218,24 @@ def test_tiny_incremental_prefill_equals_batched_bitwise(tiny):
             _, step = m.forward([t], n_past=i, want_logits=True)
         assert np.array_equal(bits(np.frombuffer(batched, dtype=np.float32)),
                               bits(np.frombuffer(step, dtype=np.float32)))
+
+
+def test_reference_order_attention_kernels_agree(tiny):
+    # Reference-order attention has two kernels: rows whose V fits in LDS
+    # (n_kv * head_dim * 4 <= 128 KB, n_kv <= 512 here) stage it there, longer
+    # ones read it from global memory. A batched 520-token prompt takes the
+    # second; a one-token step at position 511 (n_kv 512) the first. Row 511's
+    # logits must agree bit for bit.
+    _, path = tiny
+    prompt = gg.prompt_ids(5, 520, TINY["n_vocab"])
+    V = TINY["n_vocab"]
+    with Qwen2(path, n_ctx=1024, max_tokens=len(prompt)) as m:
+        m.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
+        _, rows = m.forward(prompt, n_past=0, last_logits_only=False, want_logits=True)
+        rows = np.frombuffer(rows, dtype=np.float32).reshape(len(prompt), V)
+        m.forward(prompt[:511], n_past=0)
+        _, step = m.forward(prompt[511:512], n_past=511, want_logits=True)
+        assert np.array_equal(bits(rows[511]), bits(np.frombuffer(step, dtype=np.float32)))
 
 
 def test_norm_sum_walk_way_out_bitwise(tmp_path):

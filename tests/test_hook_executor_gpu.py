@@ -41,7 +41,7 @@ import pytest
 
 import qwen2_gguf as gg
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("hip")]  # torch initialises the device first
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PLAIN = os.path.join(ROOT, "oracle", "_ref", "mini_infer")
