@@ -59,7 +59,8 @@ struct DecodeParams {
   // Scalars first: the kernel reads them in one round of scalar loads.
   int32_t n_rep;        // Q heads per KV head
   int32_t n_head_kv;
-  int32_t n_chunks;     // head chunks per KV head (n_rep / G)
+  int32_t n_chunks;     // head chunks per KV head; chunk hc holds heads
+                        // [hc n_rep / n_chunks, (hc + 1) n_rep / n_chunks)
   int32_t gpi;          // groups per item, n_head_kv * n_chunks
   int32_t n_wg;         // workgroups with work (records)
   int32_t early;        // groups of 2..kDecodeEarlyMax workgroups merged by their first finisher

@@ -362,8 +362,11 @@ void decode_kernel(const DecodeParams p) {
   const int local = wg - wg0;
   const int gl = local / kpg, part = local - gl * kpg;
   const int g = gl / a_n_chunks, hc = gl - g * a_n_chunks;
-  const int G = a_n_rep / a_n_chunks;
-  const int head0 = g * a_n_rep + hc * G;
+  // chunk hc: heads [hc n_rep / n_chunks, (hc + 1) n_rep / n_chunks) of the
+  // KV head's n_rep (never empty, at most ceil(n_rep / n_chunks) heads)
+  const int h_lo = hc * a_n_rep / a_n_chunks;
+  const int head0 = g * a_n_rep + h_lo;
+  const int G = (hc + 1) * a_n_rep / a_n_chunks - h_lo;
   const int gid = ii * a_gpi + gl;
   unsigned* const gcnt = cset + (size_t)gid * kCtrInts;
   const bool early = a_early && kpg > 1 && kpg <= kDecodeEarlyMax;

@@ -61,11 +61,14 @@ int hip_fail(hipError_t e, const char* what) {
 //                          streams at least n ring loads (0, the default: never;
 //                          measured slower on MI355X at every shape tried, since a
 //                          claim's round trip holds up the loads issued after it)
+//   MI_HIP_DECODE_HSPLIT=0 keeps a group's heads together when every group of a
+//                          launch has one workgroup (see plan_decode)
 struct Knobs {
   int kpg = 0;
   int early = 1;
   int solo = 1;
   int claim = 0;
+  int hsplit = 1;
 };
 
 struct State {
@@ -133,29 +136,33 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Decode launch plan. Every group (item, KV head, head chunk) gets kpg
 // workgroups, in proportion to its share of the launch's sub-tiles so that the
 // launch has about one workgroup per CU; at least one, and no more than leave
-// each wave a sub-tile. A group that one workgroup's ring covers in at most
-// knobs.solo rounds gets one workgroup: its loads are one latency anyway, and
-// it saves the cross-workgroup merge. Sub-tiles are claimed from device
-// counters (balancing a group's workgroups) when some group is split and each
-// of its waves streams at least knobs.claim ring loads, so that a claim's
-// round trip hides behind a ring cycle; otherwise each workgroup owns every
-// kpg-th sub-tile of its group.
+// each wave one sub-tile. A group of at most knobs.solo rounds gets one
+// workgroup: its loads are one latency anyway, and a cross-workgroup merge
+// would cost more than it saves. When a group is
+// long enough that each of its waves streams at least knobs.claim ring loads,
+// sub-tiles are claimed dynamically (so that a claim's round trip hides behind
+// a ring cycle); otherwise each workgroup owns every kpg-th sub-tile of its
+// group.
+//
+// Head split: when every group of a launch gets one workgroup, the launch is
+// bound by each workgroup's arithmetic over its heads (its loads are one
+// latency), not by the memory system; a group of more than 4 heads is then
+// cut into two chunks of ceil(G / 2) and G - ceil(G / 2) heads, each with a
+// workgroup of its own. Both read the group's K/V rows (twice the requests,
+// served from L2 for the second), each does half the arithmetic, and no merge
+// is needed since each chunk owns its heads' outputs. Not for the matrix-core
+// kernel, whose products cover 16 head columns whatever the chunk.
 struct DecodePlan {
-  int group = 1, n_chunks = 1;
+  int group = 1, n_chunks = 1;  // heads per chunk (the widest), chunks per KV head
   int n_wg = 0;    // workgroups with work (records)
   int grid_x = 0;  // the widest item's workgroups (grid rows are items)
   bool dyn = false;     // dynamic sub-tile claims
   bool long_waves = false;  // every wave streams 4 or more sub-tiles on average
+  bool mf = false;      // matrix-core kernel
 };
 
-DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim,
-                       bool f16) {
-  DecodePlan p;
-  p.group = mi::decode_group_size(n_rep);
-  p.n_chunks = n_rep / p.group;
-  const int gpi = n_head_kv * p.n_chunks;
-  const int waves = mi::decode_wg_waves(head_dim, f16);
-  const int ring = waves * mi::decode_ring_slots(head_dim, f16);
+// Assigns kpg and the first record of every item for gpi groups per item.
+void plan_items(DecodePlan& p, mi::DecodeItem* it, int n_items, int gpi, int waves, int ring) {
   int64_t sub = 0;
   for (int i = 0; i < n_items; ++i) {
     it[i].spg = (it[i].n_kv + mi::kDecodeSub - 1) / mi::kDecodeSub;
@@ -163,6 +170,8 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   }
   const int forced = g.knobs.kpg;
   int64_t wg = 0;
+  p.dyn = false;
+  p.grid_x = 0;
   for (int i = 0; i < n_items; ++i) {
     const int64_t cap = std::max<int64_t>(1, (it[i].spg + waves - 1) / waves);
     int64_t k = forced > 0 ? forced : (int64_t)g.n_cu * it[i].spg / std::max<int64_t>(1, sub);
@@ -177,6 +186,29 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   for (int i = 0; i < n_items; ++i) p.grid_x = std::max(p.grid_x, gpi * it[i].kpg);
   p.n_wg = (int)wg;
   p.long_waves = sub >= 4 * wg * waves;
+}
+
+// max_groups: the workspace's group capacity (a head split must fit in it).
+DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim,
+                       bool f16, int max_groups) {
+  DecodePlan p;
+  p.group = mi::decode_group_size(n_rep);
+  p.n_chunks = n_rep / p.group;
+  const int waves = mi::decode_wg_waves(head_dim, f16);
+  const int ring = waves * mi::decode_ring_slots(head_dim, f16);
+  plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring);
+  const int dmode = g.decode_mode.load();
+  p.mf = dmode == MI_HIP_DECODE_MATRIX || (dmode == MI_HIP_DECODE_AUTO && (f16 || p.long_waves));
+  bool solo = g.knobs.kpg <= 0;
+  for (int i = 0; i < n_items && solo; ++i) solo = it[i].kpg == 1;
+  if (solo && g.knobs.hsplit && !p.mf && p.group > 4 &&
+      (int64_t)n_items * n_head_kv * p.n_chunks * 2 <= max_groups) {
+    // every group keeps one workgroup (each is no longer than before), and
+    // sub-tiles and workgroups both double, so long_waves (and mf) stand
+    p.group = (p.group + 1) / 2;
+    p.n_chunks *= 2;
+    plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring);
+  }
   return p;
 }
 
@@ -241,7 +273,8 @@ void ws_layout(mi_hip_workspace* ws, char* base, int groups, size_t rec_bytes) {
 // (the planner's at-least-one rounding), or the forced kpg.
 void ws_capacity(int n_head_kv, int n_rep, int head_dim, int* groups, size_t* rec_bytes) {
   const int group = mi::decode_group_size(n_rep);
-  const int64_t gr = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group);
+  // a head split doubles the groups (records stay: each holds half the heads)
+  const int64_t gr = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group) * (group > 4 ? 2 : 1);
   const int64_t wgs = g.knobs.kpg > 0 ? gr * g.knobs.kpg : g.n_cu + gr;
   *groups = (int)gr;
   *rec_bytes = (size_t)wgs * mi::decode_record_floats(head_dim, group) * sizeof(float);
@@ -441,7 +474,6 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
   int rc = resolve_kv(&items[0], &r0);
   if (rc) return rc;
   const int elt = r0.f16 ? 2 : 4;
-  const int gpi = r0.n_head_kv * (items[0].n_rep / mi::decode_group_size(items[0].n_rep));
   // Launches of up to kDecodeMaxItems consecutive items sharing the position
   // strides (the kernel's per-lane load offsets derive from them).
   int base = 0;
@@ -464,7 +496,8 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
                     "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + cnt);
     }
     const DecodePlan plan =
-        plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16);
+        plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16, ws->groups);
+    const int gpi = r0.n_head_kv * plan.n_chunks;
     const int team = mi::decode_team(r0.head_dim, r0.f16, plan.group);
     for (int i = 0; i < cnt; ++i)
       if ((p.item[i].kpg + team - 1) / team > 64 - mi::kCtrTeams)
@@ -494,9 +527,8 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
     // (knob 2 forces it: tests of the fallback for parts that start late).
     p.early = g.knobs.early == 2 || (plan.n_wg <= g.n_cu && g.knobs.early != 0);
     if ((rc = ws_next_epoch(ws, cnt * gpi, stream, &p.epoch, &p.clear_groups))) return rc;
-    const int dmode = g.decode_mode.load();
-    const bool mf = dmode == MI_HIP_DECODE_MATRIX || (dmode == MI_HIP_DECODE_AUTO && (r0.f16 || plan.long_waves));
-    hipError_t e = mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, mf, stream);
+    hipError_t e =
+        mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, plan.mf, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     base += cnt;
   }
@@ -725,6 +757,7 @@ int mi_hip_init(int device) {
   g.knobs.early = env_int("MI_HIP_DECODE_EARLY", 1);
   g.knobs.solo = env_int("MI_HIP_DECODE_SOLO", 1);
   g.knobs.claim = env_int("MI_HIP_DECODE_CLAIM", 0);
+  g.knobs.hsplit = env_int("MI_HIP_DECODE_HSPLIT", 1);
   g.ready = true;
   // The default workspace: head_dim up to 128, groups of up to 8 heads, up to
   // 1024 groups per launch (e.g. 32 items x 32 KV heads), ~11 MB.

@@ -88,6 +88,23 @@ def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d, decode_mode):
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F32)
 
 
+# Short contexts, where every group gets one workgroup: the vector kernel then
+# cuts groups of more than 4 heads into two chunks (7 -> 3 + 4, 5 -> 2 + 3,
+# 14 -> four chunks of 3 or 4); with kpg forced to 1 the groups stay whole.
+@pytest.mark.parametrize("n_rep,hkv,d,n_kv", [(5, 2, 64, 200), (6, 2, 128, 100), (7, 2, 64, 130),
+                                              (7, 2, 64, 383), (8, 1, 64, 17), (14, 2, 64, 256),
+                                              (16, 1, 128, 64)])
+@pytest.mark.parametrize("kpg", [0, 1])
+def test_decode_short_context_head_chunks(hip, stream, oracle, tuning, n_rep, hkv, d, n_kv, kpg,
+                                          decode_mode):
+    print("short decode", n_rep, hkv, d, n_kv, kpg, flush=True)
+    tuning(kpg=kpg)
+    q, k, v = cpu_attention.make_inputs(5150 + 3 * n_rep + d + n_kv, d, n_rep * hkv, hkv, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F32)
+
+
 # Every F16-cache kernel variant: head_dim 64 (8 waves, 4-slot ring) with
 # groups over and under 4 heads, head_dim 128 with groups of at most 4 (one
 # head slot per row, 64 KB ring) and over 4; the Qwen2.5-0.5B shape at short,
