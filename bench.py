@@ -349,6 +349,14 @@ def bench_e2e(mh):
                 nxt, _ = m.forward([nxt], n_past=len(prompt) + i)
                 ids.append(nxt)
             t2 = time.perf_counter()
+            # the same loop with every step on the device (no host round trip
+            # between steps): decode rate from a 256-id run less a 1-id run
+            dl = []
+            for n_pred in (1, 256, 1, 256):
+                t3 = time.perf_counter()
+                dev_ids = m.generate_device(prompt, n_pred)
+                dl.append(time.perf_counter() - t3)
+            dev_s = min(dl[1], dl[3]) - min(dl[0], dl[2])
             m.set_timing(True)
             m.forward(prompt, n_past=0)
             attn_pf, _, _ = m.timing()
@@ -361,6 +369,8 @@ def bench_e2e(mh):
             out[key] = {"prefill_ms": round((t1 - t0) * 1e3, 3),
                         "decode_tok_per_s": round(255 / (t2 - t1), 1),
                         "decode_ms_per_token": round((t2 - t1) * 1e3 / 255, 4),
+                        "device_loop_decode_tok_per_s": round(255 / dev_s, 1),
+                        "device_loop_ids_equal": dev_ids == ids,
                         "attn_us_per_token": round(attn_dec * 1e3 / 64, 2),
                         "prefill_attn_us": round(attn_pf * 1e3, 1),
                         "ids_equal_reference": ids == gold["ids"],
@@ -569,7 +579,8 @@ def main():
     if want("e2e"):
         res["e2e"], e2e_model, e2e_dir = bench_e2e(mh)
         f = res["e2e"]["fused"]
-        print(f"# e2e 0.5B Q8_0: fused decode {f['decode_tok_per_s']} tok/s, attention "
+        print(f"# e2e 0.5B Q8_0: fused decode {f['decode_tok_per_s']} tok/s (device loop "
+              f"{f['device_loop_decode_tok_per_s']}), attention "
               f"{f['attn_us_per_token']} us/token; reference-order ids equal: "
               f"{res['e2e']['reference_order']['ids_equal_reference']}", file=sys.stderr, flush=True)
         if not args.no_cpu:

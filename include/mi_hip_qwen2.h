@@ -78,6 +78,20 @@ int mi_hip_qwen2_forward(mi_hip_qwen2* model, const int32_t* tokens, int32_t n_t
                          int32_t n_past, int32_t last_logits_only, float* logits_out,
                          int32_t* next_id);
 
+/* Greedy generation as the reference CLI runs it (src/main.cpp:462-495): one
+ * forward call over prompt[0..n_prompt) at position 0, then one call per
+ * further id, each on the id before it, until n_predict ids (the first from
+ * the prompt call) or until the cache's n_ctx positions are used. The ids
+ * (n_predict at most, count in *n_out) are the same as those of calling
+ * mi_hip_qwen2_forward once per token; here each step's embedding reads the
+ * previous step's greedy id from device memory, so the steps run back to back
+ * on the device without a host round trip between them, and the ids come
+ * back in one copy. Every call starts from position 0. Per-layer attention
+ * timing does not apply to it. No counterpart in the reference (its loop
+ * samples on the host between calls). */
+int mi_hip_qwen2_generate(mi_hip_qwen2* model, const int32_t* prompt, int32_t n_prompt,
+                          int32_t n_predict, int32_t* out_ids, int32_t* n_out);
+
 /* Attention kernels of the forward calls.
  *   MI_HIP_QWEN2_ATTN_FUSED (default): the throughput kernels of mi_hip_attn.h
  *     (split-KV decode, MFMA prefill; within 1e-4 of the reference ops).

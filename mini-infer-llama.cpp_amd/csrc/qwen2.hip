@@ -220,9 +220,10 @@ struct mi_hip_qwen2 {
   float *x = nullptr, *qkv = nullptr, *ao = nullptr, *gu = nullptr, *logits = nullptr;
   char* aq = nullptr;
   int32_t *ids = nullptr, *next = nullptr;
+  int32_t* gen = nullptr;      // greedy ids of a device-resident generation loop (n_ctx + 1)
   float* arg_v = nullptr;      // argmax: one (value, index) per chunk
   int32_t* arg_i = nullptr;
-  int32_t *h_ids = nullptr, *h_next = nullptr;  // pinned staging
+  int32_t *h_ids = nullptr, *h_next = nullptr, *h_gen = nullptr;  // pinned staging
   float* rope_cs = nullptr;  // (cos, sin) of every (position < n_ctx, pair), from the host's libm
   int attn_mode = MI_HIP_QWEN2_ATTN_FUSED;
   hipStream_t stream = nullptr;
@@ -272,6 +273,7 @@ void destroy(mi_hip_qwen2* m) {
   mi::rt_free(m->abuf, m->abytes);
   if (m->h_ids) (void)hipHostFree(m->h_ids);
   if (m->h_next) (void)hipHostFree(m->h_next);
+  if (m->h_gen) (void)hipHostFree(m->h_gen);
   if (m->stream) (void)hipStreamDestroy(m->stream);
   delete m;
 }
@@ -435,6 +437,7 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   const size_t olog = a; a = mi::align256(a + 4 * V * T);
   const size_t oids = a; a = mi::align256(a + 4 * T);
   const size_t onext = a; a = mi::align256(a + 4);
+  const size_t ogen = a; a = mi::align256(a + 4 * ((size_t)n_ctx + 1));
   const size_t oarg = a; a = mi::align256(a + 8 * mi::kArgmaxParts);
   const size_t ocs = a; a = mi::align256(a + 4 * 2 * (size_t)n_ctx * (hd / 2));
   if ((rc = mi::rt_alloc(&p, a, "qwen2 activations"))) return rc;
@@ -448,6 +451,7 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   m->logits = reinterpret_cast<float*>(m->abuf + olog);
   m->ids = reinterpret_cast<int32_t*>(m->abuf + oids);
   m->next = reinterpret_cast<int32_t*>(m->abuf + onext);
+  m->gen = reinterpret_cast<int32_t*>(m->abuf + ogen);
   m->arg_v = reinterpret_cast<float*>(m->abuf + oarg);
   m->arg_i = reinterpret_cast<int32_t*>(m->abuf + oarg + 4 * mi::kArgmaxParts);
   m->rope_cs = reinterpret_cast<float*>(m->abuf + ocs);
@@ -466,6 +470,7 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   }
   Q2_TRY(hipHostMalloc((void**)&m->h_ids, 4 * T, hipHostMallocDefault), "hipHostMalloc");
   Q2_TRY(hipHostMalloc((void**)&m->h_next, 4, hipHostMallocDefault), "hipHostMalloc");
+  Q2_TRY(hipHostMalloc((void**)&m->h_gen, 4 * ((size_t)n_ctx + 1), hipHostMallocDefault), "hipHostMalloc");
   Q2_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate");
   m->ev.resize(2 * L);
   for (hipEvent_t& e : m->ev) Q2_TRY(hipEventCreate(&e), "hipEventCreate");
@@ -563,18 +568,20 @@ int quantize_cols(const mi_hip_qwen2* m, const float* src, int64_t ne0, int64_t 
   return e == hipSuccess ? MI_HIP_OK : mi::rt_hip_fail(e, "qwen2 quantize launch");
 }
 
-int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last_only,
-            float* logits_out, int32_t* next_id) {
+// Enqueues one forward pass on the model's stream, nothing waited for: the T
+// token ids are read from device memory (ids_dev), the logits of the returned
+// positions land in m->logits and the greedy id of the last one in next_dev.
+// timed: bracket every layer's attention with the model's events.
+int enqueue_forward(mi_hip_qwen2* m, const int32_t* ids_dev, int T, int n_past, bool last_only,
+                    int32_t* next_dev, bool timed) {
   const mi_hip_qwen2_hparams& hp = m->hp;
   const int E = hp.n_embd, F = hp.n_ff, hd = hp.head_dim, H = hp.n_head;
   const int64_t qkv_rows = E + 2 * m->kvd;
   const int64_t ab_f = F / 32 * 36;
   hipStream_t st = m->stream;
   int rc;
-  std::memcpy(m->h_ids, tokens, 4 * (size_t)T);
-  Q2_TRY(hipMemcpyAsync(m->ids, m->h_ids, 4 * (size_t)T, hipMemcpyHostToDevice, st), "ids upload");
   hipLaunchKernelGGL(mi::embed_kernel, dim3((E + 255) / 256, T), dim3(256), 0, st, m->tok_embd,
-                     m->tok_row_bytes, m->tok_type, m->ids, m->x, E);
+                     m->tok_row_bytes, m->tok_type, ids_dev, m->x, E);
   Q2_TRY(hipGetLastError(), "embed launch");
   const float scale = 1.0f / std::sqrt((float)hd);
   for (int l = 0; l < hp.n_layer; ++l) {
@@ -641,7 +648,7 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
     aa.n_tokens = T;
     aa.scale = scale;
     aa.stream = st;
-    if (m->timing) Q2_TRY(hipEventRecord(m->ev[2 * l], st), "hipEventRecord");
+    if (timed) Q2_TRY(hipEventRecord(m->ev[2 * l], st), "hipEventRecord");
     if (m->attn_mode == MI_HIP_QWEN2_ATTN_REFERENCE_ORDER) {
       void* kd = nullptr;
       void* vd = nullptr;
@@ -672,7 +679,7 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
     } else if ((rc = mi_hip_attn_fwd(&aa))) {
       return rc;
     }
-    if (m->timing) Q2_TRY(hipEventRecord(m->ev[2 * l + 1], st), "hipEventRecord");
+    if (timed) Q2_TRY(hipEventRecord(m->ev[2 * l + 1], st), "hipEventRecord");
     if ((rc = proj(m, w.wo, m->row_e, E, E, {m->ao, nullptr}, T, m->x, E, m->x, E))) return rc;
     bool swiglued = false;
     if ((rc = proj(m, w.wgu, m->row_e, 2 * (int64_t)F, E, {m->x, w.ffn_norm}, T, m->gu, 2 * (int64_t)F,
@@ -695,8 +702,20 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
   hipLaunchKernelGGL(mi::argmax_part_kernel, dim3(mi::kArgmaxParts), dim3(mi::kArgmaxThreads), 0, st, last_row,
                      hp.n_vocab, (reinterpret_cast<uintptr_t>(last_row) & 15) == 0 ? 1 : 0, m->arg_v, m->arg_i);
   Q2_TRY(hipGetLastError(), "argmax launch");
-  hipLaunchKernelGGL(mi::argmax_final_kernel, dim3(1), dim3(mi::kWave), 0, st, last_row, m->arg_v, m->arg_i, m->next);
+  hipLaunchKernelGGL(mi::argmax_final_kernel, dim3(1), dim3(mi::kWave), 0, st, last_row, m->arg_v, m->arg_i, next_dev);
   Q2_TRY(hipGetLastError(), "argmax merge launch");
+  return MI_HIP_OK;
+}
+
+int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last_only,
+            float* logits_out, int32_t* next_id) {
+  const mi_hip_qwen2_hparams& hp = m->hp;
+  hipStream_t st = m->stream;
+  std::memcpy(m->h_ids, tokens, 4 * (size_t)T);
+  Q2_TRY(hipMemcpyAsync(m->ids, m->h_ids, 4 * (size_t)T, hipMemcpyHostToDevice, st), "ids upload");
+  int rc = enqueue_forward(m, m->ids, T, n_past, last_only, m->next, m->timing);
+  if (rc) return rc;
+  const int n_out = last_only ? 1 : T;
   Q2_TRY(hipMemcpyAsync(m->h_next, m->next, 4, hipMemcpyDeviceToHost, st), "next id copy");
   if (logits_out)
     Q2_TRY(hipMemcpyAsync(logits_out, m->logits, 4 * (size_t)hp.n_vocab * n_out, hipMemcpyDeviceToHost, st),
@@ -710,6 +729,29 @@ int forward(mi_hip_qwen2* m, const int32_t* tokens, int T, int n_past, bool last
       m->attn_ms += ms;
     }
   }
+  return MI_HIP_OK;
+}
+
+// The reference CLI's greedy loop (src/main.cpp:462-495) with every step on
+// the device: the prompt's forward call, then one forward call per further
+// id, each step's embedding reading the id the previous step's argmax wrote
+// (m->gen[i - 1]), so steps follow one another on the stream without a host
+// round trip; the ids come back in one copy at the end. Same ids as calling
+// forward once per token.
+int generate(mi_hip_qwen2* m, const int32_t* prompt, int n_prompt, int n_predict, int32_t* out_ids,
+             int32_t* n_out) {
+  hipStream_t st = m->stream;
+  std::memcpy(m->h_ids, prompt, 4 * (size_t)n_prompt);
+  Q2_TRY(hipMemcpyAsync(m->ids, m->h_ids, 4 * (size_t)n_prompt, hipMemcpyHostToDevice, st), "ids upload");
+  int rc = enqueue_forward(m, m->ids, n_prompt, 0, true, m->gen, false);
+  if (rc) return rc;
+  int n = n_predict > 0 ? 1 : 0, n_past = n_prompt;
+  for (; n < n_predict && n_past < m->n_ctx; ++n, ++n_past)
+    if ((rc = enqueue_forward(m, m->gen + n - 1, 1, n_past, true, m->gen + n, false))) return rc;
+  if (n > 0) Q2_TRY(hipMemcpyAsync(m->h_gen, m->gen, 4 * (size_t)n, hipMemcpyDeviceToHost, st), "ids copy");
+  Q2_TRY(hipStreamSynchronize(st), "hipStreamSynchronize");
+  std::memcpy(out_ids, m->h_gen, 4 * (size_t)n);
+  *n_out = n;
   return MI_HIP_OK;
 }
 
@@ -761,6 +803,21 @@ int mi_hip_qwen2_forward(mi_hip_qwen2* model, const int32_t* tokens, int32_t n_t
   model->fwd_ms += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
   model->n_calls++;
   return MI_HIP_OK;
+}
+
+int mi_hip_qwen2_generate(mi_hip_qwen2* model, const int32_t* prompt, int32_t n_prompt, int32_t n_predict,
+                          int32_t* out_ids, int32_t* n_out) {
+  if (!model || !prompt || !n_out || (n_predict > 0 && !out_ids))
+    return rt_fail(MI_HIP_E_INVALID, "model, prompt, n_out (and out_ids when n_predict > 0) must be non-NULL");
+  *n_out = 0;
+  if (n_prompt <= 0 || n_prompt > model->max_tokens)
+    return rt_fail(MI_HIP_E_INVALID, ("n_prompt must be in [1, " + std::to_string(model->max_tokens) + "]").c_str());
+  for (int i = 0; i < n_prompt; ++i)
+    if (prompt[i] < 0 || prompt[i] >= model->hp.n_vocab)
+      return rt_fail(MI_HIP_E_INVALID, ("token id " + std::to_string(prompt[i]) + " outside the vocabulary").c_str());
+  int rc = mi::rt_bind();
+  if (rc) return rc;
+  return generate(model, prompt, n_prompt, n_predict, out_ids, n_out);
 }
 
 int mi_hip_qwen2_set_attention(mi_hip_qwen2* model, int32_t mode) {

@@ -203,6 +203,8 @@ SIGNATURES = {
     "mi_hip_qwen2_forward": ([_P, ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, ctypes.c_int32,
                               ctypes.c_int32, ctypes.POINTER(ctypes.c_float),
                               ctypes.POINTER(ctypes.c_int32)], _I),
+    "mi_hip_qwen2_generate": ([_P, ctypes.POINTER(ctypes.c_int32), ctypes.c_int32, ctypes.c_int32,
+                               ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32)], _I),
     "mi_hip_qwen2_set_attention": ([_P, ctypes.c_int32], _I),
     "mi_hip_qwen2_set_timing": ([_P, ctypes.c_int32], _I),
     "mi_hip_qwen2_get_timing": ([_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),

@@ -70,6 +70,18 @@ class Qwen2:
                                                         ctypes.byref(n)))
         return a.value, f.value, n.value
 
+    def generate_device(self, prompt, n_predict):
+        """The same loop with every step on the device (mi_hip_qwen2_generate):
+        each step's embedding reads the previous greedy id from device memory,
+        so no host round trip separates the steps. Same ids as generate()."""
+        ids = (ctypes.c_int32 * len(prompt))(*prompt)
+        out = (ctypes.c_int32 * max(1, n_predict))()
+        n = ctypes.c_int32()
+        self.lib.check(self.lib.mi_hip_qwen2_generate(self.h, ids, len(prompt), n_predict, out,
+                                                      ctypes.byref(n)))
+        self.n_past = len(prompt) + max(0, n.value - 1)
+        return list(out[:n.value])
+
     def generate(self, prompt, n_predict, on_token=None):
         """The reference's generation loop (src/main.cpp:474-495): n_predict ids,
         the first from the prefill call, stopping early at n_ctx."""

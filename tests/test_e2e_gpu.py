@@ -89,6 +89,48 @@ def test_greedy_ids_identical_to_reference(model05, e2e):
     assert ids == e2e["ids"], f"first difference at step {first_diff}"
 
 
+@pytest.mark.parametrize("mode", [mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER, mh.MI_HIP_QWEN2_ATTN_FUSED],
+                         ids=["reference_order", "fused"])
+def test_device_loop_ids_equal_per_call_loop(model05, e2e, mode):
+    # mi_hip_qwen2_generate: every step's embedding reads the previous step's
+    # argmax from device memory. Same ids as one forward call per token (the
+    # reference's ids in reference-order mode), and no device allocation.
+    model05.set_attention(mode)
+    lib = model05.lib
+    before = lib.alloc_stats()
+    ids = model05.generate_device(e2e["prompt"], e2e["n_predict"])
+    after = lib.alloc_stats()
+    assert after.n_malloc == before.n_malloc
+    assert model05.n_past == len(e2e["prompt"]) + e2e["n_predict"] - 1
+    if mode == mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER:
+        assert ids == e2e["ids"]
+    else:
+        assert ids == model05.generate(e2e["prompt"], e2e["n_predict"])
+
+
+def test_device_loop_stops_at_n_ctx(tiny):
+    # the reference's loop stops once the cache's positions are used
+    # (src/main.cpp:481-484): 37 prompt positions in a 48-position cache give
+    # 1 + 11 ids however many are asked for; fewer asked, fewer given
+    _, path = tiny
+    prompt = gg.prompt_ids(13, 37, TINY["n_vocab"])
+    with Qwen2(path, n_ctx=48, max_tokens=len(prompt)) as m:
+        m.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
+        per_call = m.generate(prompt, 40)
+        assert len(per_call) == 12
+        assert m.generate_device(prompt, 40) == per_call
+        assert m.generate_device(prompt, 5) == per_call[:5]
+        assert m.generate_device(prompt, 1) == per_call[:1]
+        assert m.generate_device(prompt, 0) == []
+        lib, h = m.lib, m.h
+        out, n = (ctypes.c_int32 * 4)(), ctypes.c_int32()
+        ids = (ctypes.c_int32 * 2)(5, TINY["n_vocab"])
+        assert lib.mi_hip_qwen2_generate(h, ids, 2, 4, out, ctypes.byref(n)) == 1
+        assert "vocabulary" in lib.last_error()
+        assert lib.mi_hip_qwen2_generate(h, ids, 0, 4, out, ctypes.byref(n)) == 1
+        assert lib.mi_hip_qwen2_generate(h, ids, 1, 4, None, ctypes.byref(n)) == 1
+
+
 def test_one_token_step_equals_batched_bitwise(model05, e2e):
     # reference-order mode: a one-token step (its FFN's SiLU(gate) * up formed
     # in the gate/up matrix kernel's epilogue, its norms in the matrix kernels')
