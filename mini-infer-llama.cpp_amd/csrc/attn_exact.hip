@@ -91,8 +91,95 @@ constexpr int kExactThreads = 256;
 
 // LDS of the staged kernel for rows of up to n_kv keys: the V rows (whole 1 KB
 // transfers), the probabilities, expf's table, the wave maxima and 1 / sum.
+// The V rows and the probabilities have 16 entries of room past n_kv: the
+// ordered sums read each chunk of 16 ahead of its additions, the one past
+// the last whole chunk too (read, never added).
+__host__ __device__ inline int exact_staged_vbytes(int n_kv, int d) {
+  return ((n_kv + 16) * d * 4 + 1023) & ~1023;
+}
 __host__ __device__ inline int exact_staged_lds(int n_kv, int d) {
-  return ((n_kv * d * 4 + 1023) & ~1023) + 4 * n_kv + 32 * 8 + 4 * 4 + 16;
+  return exact_staged_vbytes(n_kv, d) + 4 * (n_kv + 16) + 32 * 8 + 4 * 4 + 16;
+}
+
+// The ordered sums of the staged kernel, in chunks of 16 terms: chunk c + 1
+// is read from LDS before chunk c's additions, so that the chain of additions
+// does not wait for each read. Terms past the last whole chunk go one by one.
+// s + p[0] + p[1] + ... + p[n - 1] (p 16-byte aligned, 16 floats readable past n)
+__device__ __forceinline__ float exact_sum(const float* p, int n) {
+#pragma clang fp contract(off)
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  float s = 0.0f;
+  float4 x[4], y[4];
+  auto get = [&](float4 (&b)[4], int c) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) b[u] = p4[4 * c + u];
+  };
+  auto add = [&](const float4 (&b)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      s = s + b[u].x;
+      s = s + b[u].y;
+      s = s + b[u].z;
+      s = s + b[u].w;
+    }
+  };
+  const int nch = n >> 4;
+  get(x, 0);
+  int c = 0;
+  // (the scheduler would otherwise sink each chunk's reads below the
+  // additions before them)
+  for (; c + 1 < nch; c += 2) {
+    get(y, c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    add(x);
+    get(x, c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    add(y);
+  }
+  if (c < nch) add(x);
+  for (int i = 16 * nch; i < n; ++i) s = s + p[i];
+  return s;
+}
+
+// acc + v[0] * p[0] + v[D] * p[1] + ... + v[(n - 1) D] * p[n - 1], each
+// product and sum rounded (v: one output element's column of V rows D floats
+// apart; 16 rows and probabilities readable past n)
+template <int D>
+__device__ __forceinline__ float exact_dot(const float* v, const float* p, int n) {
+#pragma clang fp contract(off)
+  const float4* p4 = reinterpret_cast<const float4*>(p);
+  float acc = 0.0f;
+  float va[16], vb[16];
+  float4 pa[4], pb[4];
+  auto get = [&](float (&vv)[16], float4 (&pp)[4], int c) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) vv[u] = v[(16 * c + u) * D];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) pp[u] = p4[4 * c + u];
+  };
+  auto mac = [&](const float (&vv)[16], const float4 (&pp)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc = acc + vv[4 * u] * pp[u].x;
+      acc = acc + vv[4 * u + 1] * pp[u].y;
+      acc = acc + vv[4 * u + 2] * pp[u].z;
+      acc = acc + vv[4 * u + 3] * pp[u].w;
+    }
+  };
+  const int nch = n >> 4;
+  get(va, pa, 0);
+  int c = 0;
+  for (; c + 1 < nch; c += 2) {
+    get(vb, pb, c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mac(va, pa);
+    get(va, pa, c + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    mac(vb, pb);
+  }
+  if (c < nch) mac(va, pa);
+  for (int t = 16 * nch; t < n; ++t) acc = acc + v[t * D] * p[t];
+  return acc;
 }
 
 // D: head_dim (64 or 128), so that a key's row loads are all issued at once.
@@ -107,7 +194,7 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const 
   const int kvh = h / p.n_rep;
   const int a = min(p.n_past + j + 1, p.n_past + p.n_tokens);
   const int n_kv = p.n_past + p.n_tokens;
-  const int vbytes = (n_kv * D * 4 + 1023) & ~1023;
+  const int vbytes = exact_staged_vbytes(n_kv, D);
   float* const vl = reinterpret_cast<float*>(ex_lds);  // V row t at vl + t D
   float* const prob = reinterpret_cast<float*>(ex_lds + vbytes);
   uint64_t* const tab = reinterpret_cast<uint64_t*>(ex_lds + vbytes + 4 * n_kv);
@@ -161,8 +248,7 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const 
   for (int i = tid; i < a; i += kExactThreads) prob[i] = expf_ref(prob[i] - mx, tab);
   __syncthreads();
   if (tid == 0) {
-    float sum = 0.0f;
-    for (int i = 0; i < a; ++i) sum = sum + prob[i];
+    const float sum = exact_sum(prob, a);
     red[4] = (float)(1.0 / (double)sum);  // the correctly rounded 1.0f / sum
   }
   __syncthreads();
@@ -171,8 +257,7 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const 
   wait_vmem<0>();  // this wave's V requests have landed
   __syncthreads();
   if (tid < D) {
-    float acc = 0.0f;
-    for (int t = 0; t < a; ++t) acc = acc + vl[t * D + tid] * prob[t];
+    const float acc = exact_dot<D>(vl + tid, prob, a);
     float* out = reinterpret_cast<float*>(p.out + h * p.o_s1 + (int64_t)j * p.o_s2);
     out[tid] = acc;
   }

@@ -262,22 +262,29 @@ def test_tiny_incremental_prefill_equals_batched_bitwise(tiny):
                               bits(np.frombuffer(step, dtype=np.float32)))
 
 
-def test_reference_order_attention_kernels_agree(tiny):
+@pytest.mark.parametrize("head_dim,n_prompt,steps", [
+    (64, 520, (511, 500, 271, 16, 3, 0)),
+    (128, 300, (255, 200, 100, 40, 20, 15))])
+def test_reference_order_attention_kernels_agree(tmp_path, head_dim, n_prompt, steps):
     # Reference-order attention has two kernels: rows whose V fits in LDS
-    # (n_kv * head_dim * 4 <= 128 KB, n_kv <= 512 here) stage it there, longer
-    # ones read it from global memory. A batched 520-token prompt takes the
-    # second; a one-token step at position 511 (n_kv 512) the first. Row 511's
-    # logits must agree bit for bit.
-    _, path = tiny
-    prompt = gg.prompt_ids(5, 520, TINY["n_vocab"])
-    V = TINY["n_vocab"]
+    # (n_kv * head_dim * 4 <= 128 KB: n_kv <= 512 at head_dim 64, 256 at 128)
+    # stage it there, longer ones read it from global memory. A batched prompt
+    # longer than that takes the second for every row; one-token steps at the
+    # positions in `steps` (over the cache the batched call wrote) the first,
+    # with key counts that are and are not multiples of its chunks of 16, in
+    # odd and even numbers of chunks. The rows' logits must agree bit for bit.
+    cfg = dict(TINY, n_embd=4 * head_dim, n_ff=8 * head_dim)
+    path = str(tmp_path / "m.gguf")
+    gg.write_qwen2_q8_0(path, 17, cfg)
+    prompt = gg.prompt_ids(5, n_prompt, cfg["n_vocab"])
+    V = cfg["n_vocab"]
     with Qwen2(path, n_ctx=1024, max_tokens=len(prompt)) as m:
         m.set_attention(mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER)
         _, rows = m.forward(prompt, n_past=0, last_logits_only=False, want_logits=True)
         rows = np.frombuffer(rows, dtype=np.float32).reshape(len(prompt), V)
-        m.forward(prompt[:511], n_past=0)
-        _, step = m.forward(prompt[511:512], n_past=511, want_logits=True)
-        assert np.array_equal(bits(rows[511]), bits(np.frombuffer(step, dtype=np.float32)))
+        for p in steps:
+            _, step = m.forward(prompt[p:p + 1], n_past=p, want_logits=True)
+            assert np.array_equal(bits(rows[p]), bits(np.frombuffer(step, dtype=np.float32))), p
 
 
 def test_norm_sum_walk_way_out_bitwise(tmp_path):
