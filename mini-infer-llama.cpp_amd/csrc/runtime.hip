@@ -61,14 +61,16 @@ int hip_fail(hipError_t e, const char* what) {
 //                          streams at least n ring loads (0, the default: never;
 //                          measured slower on MI355X at every shape tried, since a
 //                          claim's round trip holds up the loads issued after it)
-//   MI_HIP_DECODE_HSPLIT=0 keeps a group's heads together when every group of a
-//                          launch has one workgroup (see plan_decode)
+//   MI_HIP_DECODE_HSPLIT=0 keeps a group's heads together in every launch; 1 cuts
+//                          them only when every group of a launch has one
+//                          workgroup; 2 (the default) also in small launches
+//                          whose groups merge a few parts (see plan_decode)
 struct Knobs {
   int kpg = 0;
   int early = 1;
   int solo = 1;
   int claim = 0;
-  int hsplit = 1;
+  int hsplit = 2;
 };
 
 struct State {
@@ -150,7 +152,13 @@ constexpr float kLog2e = 1.4426950408889634f;
 // cut into two chunks of ceil(G / 2) and G - ceil(G / 2) heads, each with a
 // workgroup of its own. Both read the group's K/V rows (twice the requests,
 // served from L2 for the second), each does half the arithmetic, and no merge
-// is needed since each chunk owns its heads' outputs. Not for the matrix-core
+// is needed since each chunk owns its heads' outputs. The same holds for small
+// launches whose groups have 2..kDecodeEarlyMax parts, as long as the doubled
+// launch keeps at most one workgroup per CU: each part then streams its
+// positions for half the heads, and each chunk's parts merge among themselves
+// (one layer of the 0.5B shape from HBM, n_kv 257..1024: 7.2-8.0 -> 6.6-7.0 us
+// per launch; launches of 24 layers are left whole: splitting their 240
+// workgroups into 192 cost 1.9 us at n_kv 1024). Not for the matrix-core
 // kernel, whose products cover 16 head columns whatever the chunk.
 constexpr int64_t kDecodePartBytes = 128 << 10;
 
@@ -215,8 +223,14 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
   const int dmode = g.decode_mode.load();
   p.mf = dmode == MI_HIP_DECODE_MATRIX || (dmode == MI_HIP_DECODE_AUTO && (f16 || p.long_waves));
-  bool solo = g.knobs.kpg <= 0;
-  for (int i = 0; i < n_items && solo; ++i) solo = it[i].kpg == 1;
+  // hsplit 2: also small launches whose groups merge a few parts (early
+  // merge), while the doubled launch keeps at most one workgroup per CU
+  bool solo = g.knobs.kpg <= 0, parts = false;
+  for (int i = 0; i < n_items && solo; ++i) {
+    solo = it[i].kpg <= mi::kDecodeEarlyMax;
+    parts = parts || it[i].kpg > 1;
+  }
+  if (parts && (g.knobs.hsplit < 2 || 2 * p.n_wg > g.n_cu)) solo = false;
   if (solo && g.knobs.hsplit && !p.mf && p.group > 4 &&
       (int64_t)n_items * n_head_kv * p.n_chunks * 2 <= max_groups) {
     // every group keeps one workgroup (each is no longer than before), and
@@ -773,7 +787,7 @@ int mi_hip_init(int device) {
   g.knobs.early = env_int("MI_HIP_DECODE_EARLY", 1);
   g.knobs.solo = env_int("MI_HIP_DECODE_SOLO", 1);
   g.knobs.claim = env_int("MI_HIP_DECODE_CLAIM", 0);
-  g.knobs.hsplit = env_int("MI_HIP_DECODE_HSPLIT", 1);
+  g.knobs.hsplit = env_int("MI_HIP_DECODE_HSPLIT", 2);
   g.ready = true;
   // The default workspace: head_dim up to 128, groups of up to 8 heads, up to
   // 1024 groups per launch (e.g. 32 items x 32 KV heads), ~11 MB.
