@@ -63,8 +63,8 @@ int hip_fail(hipError_t e, const char* what) {
 //                          claim's round trip holds up the loads issued after it)
 //   MI_HIP_DECODE_HSPLIT=0 keeps a group's heads together in every launch; 1 cuts
 //                          them only when every group of a launch has one
-//                          workgroup; 2 (the default) also in small launches
-//                          whose groups merge a few parts (see plan_decode)
+//                          workgroup; 2 (the default) also in launches whose
+//                          groups merge parts (see plan_decode)
 struct Knobs {
   int kpg = 0;
   int early = 1;
@@ -152,14 +152,16 @@ constexpr float kLog2e = 1.4426950408889634f;
 // cut into two chunks of ceil(G / 2) and G - ceil(G / 2) heads, each with a
 // workgroup of its own. Both read the group's K/V rows (twice the requests,
 // served from L2 for the second), each does half the arithmetic, and no merge
-// is needed since each chunk owns its heads' outputs. The same holds for small
-// launches whose groups have 2..kDecodeEarlyMax parts, as long as the doubled
-// launch keeps at most one workgroup per CU: each part then streams its
+// is needed since each chunk owns its heads' outputs. The same holds for
+// launches whose groups merge parts, as long as the split keeps every group's
+// part count (so its workgroups double and no part streams more than before)
+// and the launch within one workgroup per CU: each part then streams its
 // positions for half the heads, and each chunk's parts merge among themselves
 // (one layer of the 0.5B shape from HBM, n_kv 257..1024: 7.2-8.0 -> 6.6-7.0 us
-// per launch; launches of 24 layers are left whole: splitting their 240
-// workgroups into 192 cost 1.9 us at n_kv 1024). Not for the matrix-core
-// kernel, whose products cover 16 head columns whatever the chunk.
+// per launch, 2048: 7.8 -> 7.1, 4096: 8.05 -> 7.5; at n_kv 8192, where the
+// split halves the part count, 8.9 -> 9.1, and 24 layers at n_kv 1024, 240
+// workgroups into 192, 12.24 -> 14.13 us: those stay whole). Not for the
+// matrix-core kernel, whose products cover 16 head columns whatever the chunk.
 constexpr int64_t kDecodePartBytes = 128 << 10;
 
 struct DecodePlan {
@@ -223,21 +225,32 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
   const int dmode = g.decode_mode.load();
   p.mf = dmode == MI_HIP_DECODE_MATRIX || (dmode == MI_HIP_DECODE_AUTO && (f16 || p.long_waves));
-  // hsplit 2: also small launches whose groups merge a few parts (early
-  // merge), while the doubled launch keeps at most one workgroup per CU
-  bool solo = g.knobs.kpg <= 0, parts = false;
-  for (int i = 0; i < n_items && solo; ++i) {
-    solo = it[i].kpg <= mi::kDecodeEarlyMax;
-    parts = parts || it[i].kpg > 1;
-  }
-  if (parts && (g.knobs.hsplit < 2 || 2 * p.n_wg > g.n_cu)) solo = false;
-  if (solo && g.knobs.hsplit && !p.mf && p.group > 4 &&
+  // Head split. hsplit 1: only when every group has one workgroup; 2: also
+  // when groups merge parts, if the split launch keeps every item's parts
+  // (its workgroups double, none streams more than before) within one
+  // workgroup per CU.
+  if (g.knobs.kpg <= 0 && g.knobs.hsplit && !p.mf && p.group > 4 &&
       (int64_t)n_items * n_head_kv * p.n_chunks * 2 <= max_groups) {
-    // every group keeps one workgroup (each is no longer than before), and
-    // sub-tiles and workgroups both double, so long_waves (and mf) stand
-    p.group = (p.group + 1) / 2;
-    p.n_chunks *= 2;
-    plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
+    int32_t kpg0[mi::kDecodeMaxItems];
+    bool solo = true;
+    for (int i = 0; i < n_items; ++i) {
+      kpg0[i] = it[i].kpg;
+      solo = solo && kpg0[i] == 1;
+    }
+    if (solo || (g.knobs.hsplit >= 2 && 2 * p.n_wg <= g.n_cu)) {
+      DecodePlan q = p;
+      q.group = (p.group + 1) / 2;
+      q.n_chunks = p.n_chunks * 2;
+      plan_items(q, it, n_items, n_head_kv * q.n_chunks, waves, ring, pos_bytes);
+      bool keep = true;
+      for (int i = 0; i < n_items; ++i) keep = keep && it[i].kpg >= kpg0[i];
+      if (keep) {
+        q.mf = p.mf;  // sub-tiles and workgroups both double: long_waves stands
+        p = q;
+      } else {
+        plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
+      }
+    }
   }
   return p;
 }

@@ -90,13 +90,15 @@ def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d, decode_mode):
 
 # Short contexts, where every group gets one workgroup: the vector kernel then
 # cuts groups of more than 4 heads into two chunks (7 -> 3 + 4, 5 -> 2 + 3,
-# 14 -> four chunks of 3 or 4), as it does for small launches whose groups
-# merge 2..8 parts (n_kv 383..1000 here: each chunk's parts merge among
-# themselves); with kpg forced to 1 the groups stay whole.
+# 14 -> four chunks of 3 or 4), as it does for launches whose groups merge
+# parts when the split keeps their part counts (n_kv 383..4096 here, early and
+# flat merges: each chunk's parts merge among themselves); with kpg forced to 1
+# the groups stay whole.
 @pytest.mark.parametrize("n_rep,hkv,d,n_kv", [(5, 2, 64, 200), (6, 2, 128, 100), (7, 2, 64, 130),
                                               (7, 2, 64, 383), (8, 1, 64, 17), (14, 2, 64, 256),
                                               (16, 1, 128, 64), (7, 2, 64, 512), (7, 2, 64, 1000),
-                                              (5, 2, 64, 777), (14, 2, 64, 700)])
+                                              (5, 2, 64, 777), (14, 2, 64, 700), (7, 2, 64, 2048),
+                                              (7, 2, 64, 4096), (7, 1, 64, 3000)])
 @pytest.mark.parametrize("kpg", [0, 1])
 def test_decode_short_context_head_chunks(hip, stream, oracle, tuning, n_rep, hkv, d, n_kv, kpg,
                                           decode_mode):
