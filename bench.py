@@ -420,8 +420,11 @@ def cpu_share():
 
 
 def cpu_info():
-    """The host CPU: model string, logical CPUs (nproc), physical cores."""
+    """The host CPU: model string (with the family / model / stepping numbers,
+    which name the part where a virtualised host shortens the string),
+    logical CPUs (nproc), physical cores."""
     model, cores = "unknown", set()
+    ids = {}
     phys = core = None
     try:
         for line in open("/proc/cpuinfo"):
@@ -429,6 +432,8 @@ def cpu_info():
             k, v = k.strip(), v.strip()
             if k == "model name" and model == "unknown":
                 model = v
+            elif k in ("vendor_id", "cpu family", "model", "stepping") and k not in ids:
+                ids[k] = v
             elif k == "physical id":
                 phys = v
             elif k == "core id":
@@ -440,6 +445,9 @@ def cpu_info():
             cores.add((phys, core))
     except OSError:
         pass
+    if ids:
+        model += " (%s)" % ", ".join("%s %s" % (k, ids[k]) for k in ("vendor_id", "cpu family", "model", "stepping")
+                                     if k in ids)
     return dict(cpu=model, nproc=os.cpu_count() or 1, physical_cores=len(cores) or None)
 
 
