@@ -224,7 +224,9 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   const int pos_bytes = 2 * head_dim * (f16 ? 2 : 4);
   plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
   const int dmode = g.decode_mode.load();
-  p.mf = dmode == MI_HIP_DECODE_MATRIX || (dmode == MI_HIP_DECODE_AUTO && (f16 || p.long_waves));
+  const bool autom = dmode == MI_HIP_DECODE_AUTO;
+  p.mf = dmode == MI_HIP_DECODE_MATRIX || (autom && p.long_waves);
+  bool split = false;
   // Head split. hsplit 1: only when every group has one workgroup; 2: also
   // when groups merge parts, if the split launch keeps every item's parts
   // (its workgroups double, none streams more than before) within one
@@ -247,11 +249,17 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
       if (keep) {
         q.mf = p.mf;  // sub-tiles and workgroups both double: long_waves stands
         p = q;
+        split = true;
       } else {
         plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
       }
     }
   }
+  // An F16 cache runs on the vector units only where its heads were split
+  // (one layer of the 0.5B shape, n_kv 256-8192: 6.5-9.1 us against 6.8-9.6
+  // with the matrix products, which win at 512, 16384, for 24 layers and for
+  // the 7B shape at n_kv 4096 and 8192, where the split does not apply).
+  if (autom && f16 && !split) p.mf = true;
   return p;
 }
 
