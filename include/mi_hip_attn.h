@@ -166,10 +166,11 @@ int mi_hip_set_prefill_mode(int32_t mode);
  *     relative per product.
  *   MI_HIP_DECODE_VALU: float multiply-adds on the vector units (exact
  *     float products).
- *   MI_HIP_DECODE_AUTO (the default): per launch, the matrix cores with an
- *     F16 cache and for F32 launches whose waves stream at least 4 sub-tiles
- *     of 16 positions each; the vector units otherwise (there the split
- *     operands' latency costs more than the products save).
+ *   MI_HIP_DECODE_AUTO (the default): per launch, the matrix cores for
+ *     launches whose waves stream at least 4 sub-tiles of 16 positions each,
+ *     and with an F16 cache unless the launch's heads are split between
+ *     workgroups (a vector-unit form); the vector units otherwise (there the
+ *     split operands' latency costs more than the products save).
  * All are within the 1e-4 bar of the reference ops. Process-wide. No
  * counterpart in the reference. */
 #define MI_HIP_DECODE_VALU 0
