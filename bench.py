@@ -34,6 +34,7 @@ sys.path.insert(0, PKG)
 METRIC = "decode attn GB/s (% HBM peak) @ n_kv=4096; prefill-1024 attn TFLOP/s"
 HBM_PEAK_GBPS = 8000.0
 FP32_MFMA_PEAK_TFLOPS = 157.3
+BF16_MFMA_PEAK_TFLOPS = 2500.0
 
 
 def parse():
@@ -44,8 +45,6 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--nondeterministic", action="store_true",
                     help="waves take work from a counter in the fused kernels (mi_hip_set_deterministic(0))")
-    ap.add_argument("--prefill-f32", action="store_true",
-                    help="prefill products on v_mfma_f32_32x32x2f32 instead of split bf16 pairs")
     ap.add_argument("--only", default="",
                     help="comma list: decode,streams,sweep,prefill,d7b,perlayer,q8,memread,e2e,copy (copy: the "
                          "counter calibration workload, only when named)")
@@ -314,6 +313,27 @@ def bench_memread(torch, lib, stream, steps, warmup, nbytes=1 << 30,
                 gbps_by_workgroups={str(k): round(v, 1) for k, v in per.items()})
 
 
+def bench_read_floor(torch, lib, stream, steps, warmup, nbytes, sets=7,
+                     shapes=(240, 256, 512, 1024, 2048)):
+    """The read floor of the headline step: mi_hip_memread over exactly the
+    step's cache bytes (24 layers x n_kv 4096 x 2 KV heads x (K + V) x 64 F32),
+    over `sets` buffers rotated as the decode's cache sets are, launched back
+    to back; the fastest workgroup count is the floor."""
+    bufs = [torch.empty(nbytes // 4, device="cuda").uniform_() for _ in range(sets)]
+    sums = torch.empty(max(shapes), device="cuda")
+    ptrs = [ctypes.c_void_p(b.data_ptr()) for b in bufs]
+    s = ctypes.c_void_p(sums.data_ptr())
+    per = {}
+    for n in shapes:
+        ms = run_timed(torch, lambda i: lib.check(lib.mi_hip_memread(ptrs[i % sets], nbytes, s, n, stream)),
+                       steps, warmup)
+        per[n] = ms
+    best = min(per, key=per.get)
+    return dict(bytes=nbytes, sets=sets, workgroups=best, us=per[best] * 1e3,
+                gbps=nbytes / (per[best] * 1e-3) / 1e9,
+                us_by_workgroups={str(k): round(v * 1e3, 3) for k, v in per.items()})
+
+
 E2E_SEED = 1234
 
 
@@ -337,8 +357,8 @@ def bench_e2e(mh):
            "model_sha256_ok": sha == gold["model_sha256"]}
     free = {}
     with Qwen2(path, n_ctx=2048, max_tokens=len(prompt)) as m:
-        for mode, key in ((mh.MI_HIP_QWEN2_ATTN_FUSED, "fused"),
-                          (mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER, "reference_order")):
+        for mode, key in ((mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER, "reference_order"),
+                          (mh.MI_HIP_QWEN2_ATTN_FUSED, "fused")):
             m.set_attention(mode)
             m.generate(prompt[:8], 4)  # warm-up
             t0 = time.perf_counter()
@@ -389,6 +409,7 @@ def bench_e2e(mh):
                                           if r["fused_id"] != r["ref_id"])
         out["fused"]["teacher_forced"] = {k: (round(v, 5) if isinstance(v, float) else v)
                                           for k, v in summ.items()}
+    out["default_mode"] = "reference_order"  # the engine's default at n_ctx 2048: ids equal
     return out, path, d
 
 
@@ -531,8 +552,6 @@ def main():
     lib.init(0)
     if args.nondeterministic:
         lib.check(lib.mi_hip_set_deterministic(0))
-    if args.prefill_f32:
-        lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
     torch.cuda.set_device(0)
     stream = torch.cuda.current_stream().cuda_stream
     only = set(filter(None, args.only.split(",")))
@@ -541,6 +560,17 @@ def main():
     res = {}
     if want("decode"):
         res["decode"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
+        # the other product form on the same workload (the default for an F32
+        # cache is the vector-unit kernel)
+        lib.check(lib.mi_hip_set_decode_mode(mh.MI_HIP_DECODE_MATRIX))
+        res["decode_matrix"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
+        lib.check(lib.mi_hip_set_decode_mode(mh.MI_HIP_DECODE_AUTO))
+        print(f"# decode 24x4096: vector units {res['decode']['kernel_ms'] * 1e3:.2f} us, matrix cores "
+              f"{res['decode_matrix']['kernel_ms'] * 1e3:.2f} us", file=sys.stderr, flush=True)
+        res["read_floor"] = bench_read_floor(torch, lib, stream, args.steps, args.warmup,
+                                             24 * 2 * 4096 * 2 * 64 * 4)
+        print(f"# read floor of the step's 100.7 MB: {res['read_floor']['us']:.2f} us "
+              f"({res['read_floor']['gbps']:.1f} GB/s)", file=sys.stderr, flush=True)
     if want("streams"):
         res["streams"] = bench_decode_streams(torch, mh, lib, args.steps, args.warmup)
         print(f"# decode 24x4096 over 2 streams: {res['streams']['gbps']:.1f} GB/s "
@@ -563,10 +593,10 @@ def main():
         res["prefill1024"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
         res["prefill4096"] = bench_prefill(torch, mh, lib, stream, max(10, args.steps // 10),
                                            max(2, args.warmup // 10), 4096)
-        if not args.prefill_f32:  # the float-product kernel beside the default
-            lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
-            res["prefill1024_f32"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
-            lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_SPLIT_BF16))
+        # the split-bf16 form beside the default float products
+        lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_SPLIT_BF16))
+        res["prefill1024_split"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
+        lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
         print(f"# prefill 1024: {res['prefill1024']['tflops']:.2f} TF/s, 4096: "
               f"{res['prefill4096']['tflops']:.2f} TF/s", file=sys.stderr, flush=True)
     if want("d7b"):
@@ -586,11 +616,11 @@ def main():
 
     if want("e2e"):
         res["e2e"], e2e_model, e2e_dir = bench_e2e(mh)
-        f = res["e2e"]["fused"]
-        print(f"# e2e 0.5B Q8_0: fused decode {f['decode_tok_per_s']} tok/s (device loop "
-              f"{f['device_loop_decode_tok_per_s']}), attention "
-              f"{f['attn_us_per_token']} us/token; reference-order ids equal: "
-              f"{res['e2e']['reference_order']['ids_equal_reference']}", file=sys.stderr, flush=True)
+        r, f = res["e2e"]["reference_order"], res["e2e"]["fused"]
+        print(f"# e2e 0.5B Q8_0 (default reference-order attention): decode {r['decode_tok_per_s']} tok/s "
+              f"(device loop {r['device_loop_decode_tok_per_s']}), ids equal: {r['ids_equal_reference']}, "
+              f"attention {r['attn_us_per_token']} us/token; fused: {f['decode_tok_per_s']} tok/s, "
+              f"attention {f['attn_us_per_token']} us/token", file=sys.stderr, flush=True)
         if not args.no_cpu:
             import qwen2_gguf as gg
             ids_path = os.path.join(e2e_dir, "ids.txt")
@@ -649,6 +679,22 @@ def main():
             "traffic": measured_traffic(),
             "bytes_per_launch": d["bytes"], "kernel_us": round(d["kernel_ms"] * 1e3, 3),
         }
+        if "decode_matrix" in res:
+            dm = res["decode_matrix"]
+            out["roofline"]["kernel"] = "vector units (float products, no MFMA)"
+            out["decode_matrix_24x4096"] = {
+                "what": "the same step on the matrix-core form (split-bf16 products, MI_HIP_DECODE_MATRIX)",
+                "us": round(dm["kernel_ms"] * 1e3, 3), "gbps": round(dm["kernel_gbps"], 1),
+                "frac": round(dm["kernel_gbps"] / HBM_PEAK_GBPS, 4)}
+        if "read_floor" in res:
+            rf = res["read_floor"]
+            out["roofline"]["read_floor"] = {
+                "what": "mi_hip_memread over exactly the step's 100,663,296 cache bytes, 7 buffers rotated, "
+                        "back to back; fastest workgroup count",
+                "us": round(rf["us"], 3), "gbps": round(rf["gbps"], 1),
+                "frac_of_peak": round(rf["gbps"] / HBM_PEAK_GBPS, 4), "workgroups": rf["workgroups"],
+                "us_by_workgroups": rf["us_by_workgroups"],
+                "decode_over_floor_us": round(d["kernel_ms"] * 1e3 - rf["us"], 3)}
         if "memread" in res:
             m = res["memread"]
             out["roofline"]["measured_read_ceiling"] = {
@@ -675,8 +721,7 @@ def main():
         p1, p4 = res["prefill1024"], res["prefill4096"]
         out["prefill"] = {
             "metric": "prefill-1024 causal attn TFLOP/s (14 Q / 2 KV heads, head_dim 64, F32)",
-            "products": "f32 (v_mfma_f32_32x32x2f32)" if args.prefill_f32 else
-                        "split bf16 pairs (three v_mfma_f32_32x32x16_bf16 per product, ~1e-5 relative)",
+            "products": "f32 (v_mfma_f32_32x32x2f32, the issued type)",
             "tflops_1024": round(p1["tflops"], 2), "us_1024": round(p1["kernel_ms"] * 1e3, 2),
             "tflops_4096": round(p4["tflops"], 2), "us_4096": round(p4["kernel_ms"] * 1e3, 2),
             "roofline": {"bound": "mfma", "achieved": round(p1["tflops"], 2),
@@ -684,11 +729,14 @@ def main():
                          "frac": round(p1["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
                          "flops_per_launch": p1["flops"], "mfma_counters": measured_mfma()},
         }
-        if "prefill1024_f32" in res:
-            pf = res["prefill1024_f32"]
-            out["prefill"]["f32_products_1024"] = {
-                "tflops": round(pf["tflops"], 2), "us": round(pf["kernel_ms"] * 1e3, 2),
-                "frac": round(pf["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4)}
+        if "prefill1024_split" in res:
+            ps = res["prefill1024_split"]
+            # three bf16 products per float product: issued bf16 FLOPs are 3x
+            # the causal count (plus the diagonal tiles' masked halves)
+            out["prefill"]["split_bf16_1024"] = {
+                "tflops_causal": round(ps["tflops"], 2), "us": round(ps["kernel_ms"] * 1e3, 2),
+                "issued_tflops_bf16": round(3 * ps["tflops"], 2),
+                "frac_of_bf16_peak": round(3 * ps["tflops"] / BF16_MFMA_PEAK_TFLOPS, 4)}
     if "sweep" in res:
         out["decode_sweep"] = {
             "workload": "24 independent layer caches, 1 query token, 14 Q / 2 KV heads, head_dim 64, "

@@ -145,14 +145,17 @@ int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim
 int mi_hip_set_deterministic(int32_t on);
 
 /* Matrix cores of the prefill kernel's QK and PV products.
- *   MI_HIP_PREFILL_SPLIT_BF16 (the default): every float operand is split
- *     into a pair of bf16 (hi = round(x), lo = round(x - hi), |x - hi - lo| <=
- *     2^-17 |x|) and each product is lo.hi + hi.lo + hi.hi on
- *     v_mfma_f32_32x32x16_bf16 with float accumulation: ~1e-5 relative per
- *     product, three bf16 products at 16x the FP32 matrix rate.
- *   MI_HIP_PREFILL_F32: v_mfma_f32_32x32x2f32 (float products).
- * Both are within the 1e-4 bar of the reference ops. Process-wide. No
- * counterpart in the reference. */
+ *   MI_HIP_PREFILL_F32 (the default): v_mfma_f32_32x32x2f32 (float
+ *     products, as the reference's ops), within the 1e-4 bar at any score
+ *     magnitude.
+ *   MI_HIP_PREFILL_SPLIT_BF16: every float operand is split into a pair of
+ *     bf16 (hi = round(x), lo = round(x - hi), |x - hi - lo| <= 2^-17 |x|)
+ *     and each product is lo.hi + hi.lo + hi.hi on v_mfma_f32_32x32x16_bf16
+ *     with float accumulation: ~2^-16 relative error per product, three bf16
+ *     products at 16x the FP32 matrix rate. Within the 1e-4 bar only while
+ *     scale * |q| * |k| stays small (N(0,1) inputs with q and k scaled by up
+ *     to 2).
+ * Process-wide. No counterpart in the reference. */
 #define MI_HIP_PREFILL_F32 0
 #define MI_HIP_PREFILL_SPLIT_BF16 1
 int mi_hip_set_prefill_mode(int32_t mode);
@@ -166,13 +169,14 @@ int mi_hip_set_prefill_mode(int32_t mode);
  *     relative per product.
  *   MI_HIP_DECODE_VALU: float multiply-adds on the vector units (exact
  *     float products).
- *   MI_HIP_DECODE_AUTO (the default): per launch, the matrix cores for
- *     launches whose waves stream at least 4 sub-tiles of 16 positions each,
- *     and with an F16 cache unless the launch's heads are split between
- *     workgroups (a vector-unit form); the vector units otherwise (there the
- *     split operands' latency costs more than the products save).
- * All are within the 1e-4 bar of the reference ops. Process-wide. No
- * counterpart in the reference. */
+ *   MI_HIP_DECODE_AUTO (the default): the vector units for an F32 cache;
+ *     for an F16 cache the matrix cores unless the launch's heads are split
+ *     between workgroups (a vector-unit form).
+ * The split bf16 pairs of the matrix form carry ~2^-16 relative error per
+ * product into the scores, so with an F32 cache it stays within the 1e-4 bar
+ * only while scale * |q| * |k| stays small (N(0,1) inputs with q and k
+ * scaled by up to 2); the other forms are within it at any magnitude.
+ * Process-wide. No counterpart in the reference. */
 #define MI_HIP_DECODE_VALU 0
 #define MI_HIP_DECODE_MATRIX 1
 #define MI_HIP_DECODE_AUTO 2

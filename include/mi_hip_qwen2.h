@@ -93,9 +93,12 @@ int mi_hip_qwen2_generate(mi_hip_qwen2* model, const int32_t* prompt, int32_t n_
                           int32_t n_predict, int32_t* out_ids, int32_t* n_out);
 
 /* Attention kernels of the forward calls.
- *   MI_HIP_QWEN2_ATTN_FUSED (default): the throughput kernels of mi_hip_attn.h
- *     (split-KV decode, MFMA prefill; within 1e-4 of the reference ops).
- *   MI_HIP_QWEN2_ATTN_REFERENCE_ORDER: one wave per (token, head) running the
+ *   MI_HIP_QWEN2_ATTN_FUSED: the throughput kernels of mi_hip_attn.h
+ *     (split-KV decode, MFMA prefill; within 1e-4 of the reference ops, so
+ *     greedy ids follow the reference engine's until a near-tie argmax).
+ *     The default when n_ctx > 32768.
+ *   MI_HIP_QWEN2_ATTN_REFERENCE_ORDER (the default for n_ctx <= 32768): one
+ *     wave per (token, head) running the
  *     reference's own operation order (src/ops_cpu.cpp:304-410: ordered dot
  *     products and sums, the C library's expf), bit-identical to the engine;
  *     cost linear in the context per row. With it every step of a forward call

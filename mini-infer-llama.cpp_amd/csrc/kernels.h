@@ -17,9 +17,11 @@ int decode_ring_slots(int head_dim, bool f16);          // ring slots per wave
 size_t decode_record_floats(int head_dim, int group);   // floats per cross-workgroup record
 int decode_team(int head_dim, bool f16, int group);     // workgroups per combine team
 // p.rec: one record per workgroup; p.cnt: two counter sets (the set of the
-// launch's epoch parity is zero on entry; the other is cleared). dyn: the
-// waves claim sub-tiles from the group counters (required when any item has
-// kpg > 1); otherwise each workgroup takes its group's sub-tiles from LDS.
+// launch's epoch parity is zero on entry; the other is cleared). By default
+// every workgroup, kpg > 1 included, takes fixed strided sub-tiles of its
+// group (part p: p, p + kpg, ...) through an LDS counter; dyn (opt-in,
+// MI_HIP_DECODE_CLAIM) has the waves claim sub-tiles from the group's
+// counter in device memory instead.
 // Grid (grid_x, n_items): row y serves p.item[y]; workgroups past an item's
 // gpi * kpg leave at once.
 hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,

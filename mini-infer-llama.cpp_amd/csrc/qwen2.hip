@@ -225,7 +225,7 @@ struct mi_hip_qwen2 {
   int32_t* arg_i = nullptr;
   int32_t *h_ids = nullptr, *h_next = nullptr, *h_gen = nullptr;  // pinned staging
   float* rope_cs = nullptr;  // (cos, sin) of every (position < n_ctx, pair), from the host's libm
-  int attn_mode = MI_HIP_QWEN2_ATTN_FUSED;
+  int attn_mode = MI_HIP_QWEN2_ATTN_REFERENCE_ORDER;  // FUSED when n_ctx > kExactMaxKeys
   hipStream_t stream = nullptr;
   bool timing = false;
   std::vector<hipEvent_t> ev;
@@ -311,6 +311,7 @@ int load_model(const char* path, int32_t n_ctx, int32_t max_tokens, mi_hip_qwen2
   m->kvd = hd * (int)Hkv;
   if (n_ctx <= 0) return rt_fail(MI_HIP_E_INVALID, "n_ctx must be positive");
   m->n_ctx = n_ctx;
+  if (n_ctx > mi::kExactMaxKeys) m->attn_mode = MI_HIP_QWEN2_ATTN_FUSED;
   m->max_tokens = max_tokens > 0 ? std::min(max_tokens, n_ctx) : n_ctx;
   const int64_t V = m->hp.n_vocab;
   m->row_e = E / 32 * 34;

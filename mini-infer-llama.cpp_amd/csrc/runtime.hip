@@ -82,10 +82,10 @@ struct State {
   int n_cu = 0;  // compute units of the device
   Knobs knobs;
   std::atomic<int> deterministic{1};  // fixed per-wave takes in the fused kernels
-  std::atomic<int> prefill_mode{MI_HIP_PREFILL_SPLIT_BF16};  // matrix cores of the prefill kernel
+  std::atomic<int> prefill_mode{MI_HIP_PREFILL_F32};  // matrix cores of the prefill kernel
   std::atomic<int> decode_mode{MI_HIP_DECODE_AUTO};          // matrix cores of the decode kernel
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
-  mi_hip_workspace* scratch_ws = nullptr;  // over the static scratch array (never freed)
+  mi_hip_workspace* scratch_ws = nullptr;  // this device's entry of scratch_by_device
   // Host-resident attention nodes run on the node kernels (opt-in): a staging
   // buffer that grows to the largest node seen, and a stream for it.
   std::atomic<int> host_nodes{0};
@@ -95,6 +95,13 @@ struct State {
   hipStream_t node_stream = nullptr;
 };
 State g;
+
+// The no-allocation entry point's workspace of each device, kept for the
+// life of the process like the array it lies over: its launch stamp and
+// counter-set state must continue across mi_hip_shutdown / mi_hip_init,
+// because the array keeps the records and counters of every earlier call.
+constexpr int kMaxDevices = 64;
+mi_hip_workspace* scratch_by_device[kMaxDevices] = {};
 
 int dev_alloc(void** p, size_t bytes, const char* what) {
   const uint64_t lim = g.limit.load();
@@ -225,7 +232,10 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
   plan_items(p, it, n_items, n_head_kv * p.n_chunks, waves, ring, pos_bytes);
   const int dmode = g.decode_mode.load();
   const bool autom = dmode == MI_HIP_DECODE_AUTO;
-  p.mf = dmode == MI_HIP_DECODE_MATRIX || (autom && p.long_waves);
+  // AUTO keeps an F32 cache on the vector units (float products, as the
+  // reference's ops): the matrix form splits F32 operands into bf16 pairs,
+  // whose ~2^-16 relative error per product grows with the score magnitude.
+  p.mf = dmode == MI_HIP_DECODE_MATRIX;
   bool split = false;
   // Head split. hsplit 1: only when every group has one workgroup; 2: also
   // when groups merge parts, if the split launch keeps every item's parts
@@ -521,20 +531,28 @@ mi_hip_workspace* workspace_of(const mi_hip_attn_args* a) {
 
 int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_workspace* ws) {
   if (!ws) return fail(MI_HIP_E_STATE, "no decode workspace (the library default is gone)");
+  // Each launch's stamp and counter-set parity are chosen here on the host
+  // and passed by value, so a captured launch would replay stale ones.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  MI_TRY_HIP(hipStreamIsCapturing(stream, &cap), "hipStreamIsCapturing");
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(MI_HIP_E_UNSUPPORTED,
+                "decode launches cannot be captured into a graph (each launch takes a fresh stamp)");
   Resolved r0;
   int rc = resolve_kv(&items[0], &r0);
   if (rc) return rc;
   const int elt = r0.f16 ? 2 : 4;
   // Launches of up to kDecodeMaxItems consecutive items sharing the position
-  // strides (the kernel's per-lane load offsets derive from them).
-  int base = 0;
-  while (base < n) {
-    mi::DecodeParams p{};
-    int cnt = 0;
+  // strides (the kernel's per-lane load offsets derive from them). Every
+  // launch is planned and checked against the workspace before the first is
+  // enqueued, so a refused call leaves no partial output behind.
+  auto plan_launch = [&](int base, mi::DecodeParams& p, int& cnt, DecodePlan& plan) -> int {
+    p = mi::DecodeParams{};
+    cnt = 0;
     for (; cnt < mi::kDecodeMaxItems && base + cnt < n; ++cnt) {
       Resolved r;
-      rc = resolve_kv(&items[base + cnt], &r);
-      if (rc) return rc;
+      int rc2 = resolve_kv(&items[base + cnt], &r);
+      if (rc2) return rc2;
       if (cnt > 0 && (r.k_s2 != p.item[0].k_s2 || r.v_s2 != p.item[0].v_s2)) break;
       if (r.k_s2 < (int64_t)r.head_dim * elt || r.v_s2 < (int64_t)r.head_dim * elt)
         return fail(MI_HIP_E_UNSUPPORTED, "item %d: position stride below one row", base + cnt);
@@ -546,8 +564,7 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
         return fail(MI_HIP_E_UNSUPPORTED,
                     "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + cnt);
     }
-    const DecodePlan plan =
-        plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16, ws->groups);
+    plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16, ws->groups);
     const int gpi = r0.n_head_kv * plan.n_chunks;
     const int team = mi::decode_team(r0.head_dim, r0.f16, plan.group);
     for (int i = 0; i < cnt; ++i)
@@ -577,11 +594,20 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
     // be resident at once (one per CU); it stays correct otherwise.
     // (knob 2 forces it: tests of the fallback for parts that start late).
     p.early = g.knobs.early == 2 || (plan.n_wg <= g.n_cu && g.knobs.early != 0);
-    if ((rc = ws_next_epoch(ws, cnt * gpi, stream, &p.epoch, &p.clear_groups))) return rc;
+    return MI_HIP_OK;
+  };
+  mi::DecodeParams p;
+  DecodePlan plan;
+  int cnt = 0, launches = 0;
+  for (int base = 0; base < n; base += cnt, ++launches)
+    if ((rc = plan_launch(base, p, cnt, plan))) return rc;
+  for (int base = 0; base < n; base += cnt) {
+    // (a single launch is still planned in p)
+    if (launches > 1 && (rc = plan_launch(base, p, cnt, plan))) return rc;
+    if ((rc = ws_next_epoch(ws, cnt * p.gpi, stream, &p.epoch, &p.clear_groups))) return rc;
     hipError_t e =
         mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, plan.mf, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
-    base += cnt;
   }
   return MI_HIP_OK;
 }
@@ -820,21 +846,32 @@ int mi_hip_init(int device) {
     return rc;
   }
   // The no-allocation entry point's scratch: this device's copy of the static
-  // array (zero at load, as its counters and record stamps must start).
-  void* sp = nullptr;
-  hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
-  if (se != hipSuccess || !sp) {
+  // array (zero at load, as its counters and record stamps must start). Its
+  // workspace is made once per device and never destroyed (a later session
+  // continues its stamps over the records the array still holds).
+  if (device >= kMaxDevices) {
     ws_destroy(g.default_ws);
     g.default_ws = nullptr;
     g.ready = false;
-    return hip_fail(se != hipSuccess ? se : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    return fail(MI_HIP_E_UNSUPPORTED, "device %d: at most %d devices", device, kMaxDevices);
   }
-  if ((rc = ws_over_scratch(sp, &g.scratch_ws))) {
-    ws_destroy(g.default_ws);
-    g.default_ws = nullptr;
-    g.ready = false;
-    return rc;
+  if (!scratch_by_device[device]) {
+    void* sp = nullptr;
+    hipError_t se = hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch));
+    if (se != hipSuccess || !sp) {
+      ws_destroy(g.default_ws);
+      g.default_ws = nullptr;
+      g.ready = false;
+      return hip_fail(se != hipSuccess ? se : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    }
+    if ((rc = ws_over_scratch(sp, &scratch_by_device[device]))) {
+      ws_destroy(g.default_ws);
+      g.default_ws = nullptr;
+      g.ready = false;
+      return rc;
+    }
   }
+  g.scratch_ws = scratch_by_device[device];
   t_err[0] = '\0';
   return MI_HIP_OK;
 }
@@ -847,8 +884,7 @@ int mi_hip_shutdown(void) {
   (void)hipDeviceSynchronize();
   ws_destroy(g.default_ws);
   g.default_ws = nullptr;
-  ws_destroy(g.scratch_ws);  // the array itself stays until the process ends
-  g.scratch_ws = nullptr;
+  g.scratch_ws = nullptr;  // kept in scratch_by_device, as the array keeps its contents
   {
     std::lock_guard<std::mutex> nl(g.node_mu);
     dev_free(g.node_stage, g.node_stage_bytes);

@@ -58,7 +58,8 @@ class Qwen2:
         return nxt.value, logits
 
     def set_attention(self, mode):
-        """mh.MI_HIP_QWEN2_ATTN_FUSED (default) or mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER."""
+        """mh.MI_HIP_QWEN2_ATTN_REFERENCE_ORDER (the default up to n_ctx 32768: token ids equal
+        to the reference engine's) or mh.MI_HIP_QWEN2_ATTN_FUSED (the throughput kernels)."""
         self.lib.check(self.lib.mi_hip_qwen2_set_attention(self.h, mode))
 
     def set_timing(self, on):
@@ -156,7 +157,7 @@ def main(argv=None):
     ap.add_argument("-c", "--ctx", type=int, default=2048)
     ap.add_argument("-n", "--n-predict", type=int, default=128)
     ap.add_argument("--bench", action="store_true")
-    ap.add_argument("--attention", choices=("fused", "reference-order"), default="fused",
+    ap.add_argument("--attention", choices=("fused", "reference-order"), default="reference-order",
                     help="fused: the throughput kernels; reference-order: bit-identical to the "
                          "reference engine (token ids equal)")
     a = ap.parse_args(argv)

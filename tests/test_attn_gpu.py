@@ -450,6 +450,77 @@ def test_decode_batch_24_layers(hip, stream, oracle, tuning, early, det, decode_
         assert_close(douts[layer].cpu().numpy(), want, TOL_F32, f"layer {layer}")
 
 
+# The 24-layer batched launch of the decode sweep at every n_kv it is timed
+# at (4096 above), each layer an independent cache with its own context
+# length (n_kv - layer), generated on the device. All layers are checked
+# against the oracle up to n_kv 1024, a fixed sample of six beyond (the
+# planner lays the launch out by its total work, so the sample's launch is
+# the timed one).
+@pytest.mark.parametrize("n_kv", [128, 1024, 16384, 32768])
+def test_decode_batch_24_layers_sweep(hip, stream, oracle, n_kv, decode_mode):
+    import torch
+    print("24-layer batch n_kv", n_kv, flush=True)
+    n_layers = 24
+    gen = torch.Generator(device="cuda").manual_seed(7100 + n_kv)
+    k = torch.randn((n_layers, n_kv, 2, 64), device="cuda", generator=gen)
+    v = torch.randn((n_layers, n_kv, 2, 64), device="cuda", generator=gen)
+    q = torch.randn((n_layers, 1, 14, 64), device="cuda", generator=gen)
+    out = torch.full_like(q, float("nan"))
+    items = (mh.AttnArgs * n_layers)(*[
+        mh.attn_args(q[i], out[i], 7, n_kv - 1 - i, 0.125, stream, k=k[i], v=v[i])
+        for i in range(n_layers)])
+    hip.check(hip.mi_hip_attn_decode_batch(items, n_layers, stream))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    layers = range(n_layers) if n_kv <= 1024 else (0, 1, 7, 12, 18, 23)
+    for i in layers:
+        n = n_kv - i
+        want = ref_out(oracle, q[i].cpu().numpy(), k[i, :n].cpu().numpy(), v[i, :n].cpu().numpy(),
+                       n - 1, 0.125)
+        assert_close(got[i], want, TOL_F32, f"layer {i} (n_kv {n})")
+
+
+# Scores far from N(0,1): q and k scaled by s (score standard deviation ~s^2).
+# The float-product forms (the defaults) hold the F32 bar at any magnitude;
+# the split-bf16 matrix forms (~2^-16 per product) hold it up to s = 2, the
+# limit their documentation states.
+@pytest.mark.parametrize("s", [2.0, 4.0, 8.0])
+@pytest.mark.parametrize("n_kv", [777, 4096])
+def test_decode_large_scores(hip, stream, oracle, s, n_kv, decode_mode):
+    if decode_mode == mh.MI_HIP_DECODE_MATRIX and s > 2.0:
+        pytest.skip("split-bf16 products: documented for q, k scaled by at most 2")
+    print("decode large scores", s, n_kv, decode_mode, flush=True)
+    q, k, v = cpu_attention.make_inputs(6100 + n_kv + int(s), 64, 14, 2, n_kv, 1)
+    q, k = (q * np.float32(s)).astype(np.float32), (k * np.float32(s)).astype(np.float32)
+    got = fused(hip, stream, q, k, v, n_kv - 1, 0.125)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, 0.125), TOL_F32, f"s={s}")
+
+
+@pytest.mark.parametrize("s", [2.0, 4.0, 8.0])
+def test_decode_large_scores_f16_cache(hip, stream, oracle, s):
+    # the default form for an F16 cache (matrix cores, f16 operands, Q and P
+    # split into f16 pairs), against the oracle on the widened cache
+    print("decode large scores f16", s, flush=True)
+    q, k, v = cpu_attention.make_inputs(6300 + int(s), 128, 28, 4, 4096, 1)
+    q, k = (q * np.float32(s)).astype(np.float32), (k * np.float32(s)).astype(np.float32)
+    scale = float(np.float32(1) / np.sqrt(np.float32(128)))
+    got = fused(hip, stream, q, k, v, 4095, scale, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, 4095, scale, f16=True), TOL_F32, f"s={s}")
+
+
+@pytest.mark.parametrize("s", [2.0, 4.0, 8.0])
+@pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_F32, mh.MI_HIP_PREFILL_SPLIT_BF16])
+def test_prefill_large_scores(hip, stream, oracle, prefill_mode, mode, s):
+    if mode == mh.MI_HIP_PREFILL_SPLIT_BF16 and s > 2.0:
+        pytest.skip("split-bf16 products: documented for q, k scaled by at most 2")
+    print("prefill large scores", s, mode, flush=True)
+    prefill_mode(mode)
+    q, k, v = cpu_attention.make_inputs(6200 + int(s), 64, 14, 2, 300, 300)
+    q, k = (q * np.float32(s)).astype(np.float32), (k * np.float32(s)).astype(np.float32)
+    got = fused(hip, stream, q, k, v, 0, 0.125)
+    assert_close(got, ref_out(oracle, q, k, v, 0, 0.125), TOL_F32, f"s={s}")
+
+
 @pytest.mark.parametrize("n_past,n_tok,d,h,hkv", [
     (0, 1024, 64, 14, 2),     # the prefill-1024 config, full oracle
     (0, 33, 64, 14, 2),
@@ -551,7 +622,7 @@ def prefill_mode(hip):
     def set_(mode):
         hip.check(hip.mi_hip_set_prefill_mode(mode))
     yield set_
-    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_SPLIT_BF16))
+    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
 
 
 @pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_F32, mh.MI_HIP_PREFILL_SPLIT_BF16])

@@ -5,7 +5,11 @@ Bar: |noalloc - regular| <= 1e-4 + 1e-4*|regular| (the F32 parity bar; the
 fused kernels' accumulation order follows which wave takes which sub-tile, so
 two launches agree to rounding, not bitwise). Two calls in a row, the second
 smaller, share the scratch; neither may allocate device memory, and a launch
-beyond the scratch's capacity is refused before anything runs.
+beyond the scratch's capacity is refused before anything runs. The scratch
+keeps its contents across mi_hip_shutdown / mi_hip_init, and so does the
+stamp sequence over it: a call after a new init is checked against the
+oracle. Launches under graph capture are refused (a captured launch would
+replay its stamp).
 """
 import ctypes
 
@@ -90,3 +94,40 @@ def test_noalloc_refuses_launches_beyond_its_scratch(hip, stream):
     hip.check(rc)
     torch.cuda.synchronize()
     assert np.all(np.isfinite(out.cpu().numpy()))
+
+
+def test_noalloc_after_shutdown_and_init(hip, stream):
+    # records and counters from the calls above stay in the static array; the
+    # session after a shutdown / init continues the stamps over them
+    import torch
+    q, k, v = _items(24, 4096, 15)
+    rc, first = _run(hip, hip.mi_hip_attn_decode_batch_noalloc, q, k, v, 4096, stream)
+    hip.check(rc)
+    torch.cuda.synchronize()
+    hip.check(hip.mi_hip_shutdown())
+    hip.check(hip.mi_hip_init(0))
+    for seed in (16, 17):
+        q, k, v = _items(24, 4096, seed)
+        rc, got = _run(hip, hip.mi_hip_attn_decode_batch_noalloc, q, k, v, 4096, stream)
+        hip.check(rc)
+        torch.cuda.synchronize()
+        g = got.cpu().numpy()
+        for i in (0, 11, 23):
+            want = cpu_attention.oracle().attention(q[i].cpu().numpy(), k[i, :4096 - i].cpu().numpy(),
+                                                    v[i, :4096 - i].cpu().numpy(), 4095 - i, 0.125, 8)[2]
+            _close(g[i], want, f"after init, seed {seed}, item {i}")
+
+
+def test_decode_refused_under_graph_capture(hip):
+    import torch
+    q, k, v = _items(2, 256, 18)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(g, stream=side, capture_error_mode="thread_local"):
+        st = torch.cuda.current_stream().cuda_stream
+        for fn in (hip.mi_hip_attn_decode_batch_noalloc, hip.mi_hip_attn_decode_batch):
+            rc, _ = _run(hip, fn, q, k, v, 256, st)
+            rcs.append((rc, hip.last_error()))
+    assert all(rc == 5 and "captured" in msg for rc, msg in rcs), rcs
