@@ -560,12 +560,14 @@ def main():
     res = {}
     if want("decode"):
         res["decode"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
-        # the other product form on the same workload (the default for an F32
-        # cache is the vector-unit kernel)
-        lib.check(lib.mi_hip_set_decode_mode(mh.MI_HIP_DECODE_MATRIX))
-        res["decode_matrix"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
+        # the other kernels on the same workload (the default for this launch
+        # is the streaming vector-unit kernel)
+        for key, mode in (("decode_matrix", mh.MI_HIP_DECODE_MATRIX), ("decode_stream", mh.MI_HIP_DECODE_STREAM)):
+            lib.check(lib.mi_hip_set_decode_mode(mode))
+            res[key] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
         lib.check(lib.mi_hip_set_decode_mode(mh.MI_HIP_DECODE_AUTO))
-        print(f"# decode 24x4096: vector units {res['decode']['kernel_ms'] * 1e3:.2f} us, matrix cores "
+        print(f"# decode 24x4096: vector units (default) {res['decode']['kernel_ms'] * 1e3:.2f} us, streaming "
+              f"kernel {res['decode_stream']['kernel_ms'] * 1e3:.2f} us, matrix cores "
               f"{res['decode_matrix']['kernel_ms'] * 1e3:.2f} us", file=sys.stderr, flush=True)
         res["read_floor"] = bench_read_floor(torch, lib, stream, args.steps, args.warmup,
                                              24 * 2 * 4096 * 2 * 64 * 4)
@@ -680,12 +682,18 @@ def main():
             "bytes_per_launch": d["bytes"], "kernel_us": round(d["kernel_ms"] * 1e3, 3),
         }
         if "decode_matrix" in res:
-            dm = res["decode_matrix"]
-            out["roofline"]["kernel"] = "vector units (float products, no MFMA)"
+            dm, dr = res["decode_matrix"], res["decode_stream"]
+            out["roofline"]["kernel"] = ("decode_kernel, vector units (float products, no MFMA; "
+                                         "MI_HIP_DECODE_VALU, the default for an F32 cache)")
             out["decode_matrix_24x4096"] = {
                 "what": "the same step on the matrix-core form (split-bf16 products, MI_HIP_DECODE_MATRIX)",
                 "us": round(dm["kernel_ms"] * 1e3, 3), "gbps": round(dm["kernel_gbps"], 1),
                 "frac": round(dm["kernel_gbps"] / HBM_PEAK_GBPS, 4)}
+            out["decode_stream_24x4096"] = {
+                "what": "the same step on the streaming vector-unit kernel (MI_HIP_DECODE_STREAM: K/V straight "
+                        "into registers, last-arriver merge)",
+                "us": round(dr["kernel_ms"] * 1e3, 3), "gbps": round(dr["kernel_gbps"], 1),
+                "frac": round(dr["kernel_gbps"] / HBM_PEAK_GBPS, 4)}
         if "read_floor" in res:
             rf = res["read_floor"]
             out["roofline"]["read_floor"] = {

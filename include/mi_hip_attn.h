@@ -169,9 +169,13 @@ int mi_hip_set_prefill_mode(int32_t mode);
  *     relative per product.
  *   MI_HIP_DECODE_VALU: float multiply-adds on the vector units (exact
  *     float products).
- *   MI_HIP_DECODE_AUTO (the default): the vector units for an F32 cache;
- *     for an F16 cache the matrix cores unless the launch's heads are split
- *     between workgroups (a vector-unit form).
+ *   MI_HIP_DECODE_STREAM: float multiply-adds on the vector units in the
+ *     streaming kernel (K/V straight into registers, each group's parts
+ *     merged by the last to arrive), for head_dim 64 or 128 and groups that
+ *     span several workgroups; other launches take MI_HIP_DECODE_VALU.
+ *   MI_HIP_DECODE_AUTO (the default): the vector units (MI_HIP_DECODE_VALU)
+ *     for an F32 cache; for an F16 cache the matrix cores unless the launch's
+ *     heads are split between workgroups (a vector-unit form).
  * The split bf16 pairs of the matrix form carry ~2^-16 relative error per
  * product into the scores, so with an F32 cache it stays within the 1e-4 bar
  * only while scale * |q| * |k| stays small (N(0,1) inputs with q and k
@@ -180,6 +184,7 @@ int mi_hip_set_prefill_mode(int32_t mode);
 #define MI_HIP_DECODE_VALU 0
 #define MI_HIP_DECODE_MATRIX 1
 #define MI_HIP_DECODE_AUTO 2
+#define MI_HIP_DECODE_STREAM 3
 int mi_hip_set_decode_mode(int32_t mode);
 
 /* ---- device-resident KV cache ------------------------------------------ */

@@ -69,6 +69,7 @@ struct DecodeParams {
   int32_t ctr_groups;   // groups one counter set covers
   int32_t clear_groups; // groups [0, clear_groups) of the other counter set to clear
   uint32_t epoch;       // launch stamp (nonzero, new for every launch on this workspace)
+  int32_t rec_words;    // 64-bit words per record slot (the streaming kernel)
   float scale_log2e;    // softmax scale * log2(e)
   float* rec;           // one record per workgroup
   unsigned* cnt;        // two counter sets of ctr_groups * kCtrInts words: launch e uses set

@@ -26,6 +26,13 @@ int decode_team(int head_dim, bool f16, int group);     // workgroups per combin
 // gpi * kpg leave at once.
 hipError_t launch_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,
                          bool dyn, bool mf, hipStream_t stream);
+// decode_stream.hip: the streaming decode kernel for launches whose groups
+// span several workgroups (float products, K/V straight into registers, the
+// merge by the last part to arrive). head_dim 64 or 128, F32 or F16 cache,
+// group <= 8 heads; p.rec_words >= stream_record_words(head_dim, group).
+size_t stream_record_words(int head_dim, int group);
+hipError_t launch_stream_decode(const DecodeParams& p, int grid_x, int n_items, int head_dim, bool f16, int group,
+                                hipStream_t stream);
 // n words at p set to v on `stream` (a kernel, so it may sit in a graph).
 hipError_t launch_fill_u32(unsigned* p, size_t n, unsigned v, hipStream_t stream);
 

@@ -66,6 +66,7 @@ int hip_fail(hipError_t e, const char* what) {
 //                          workgroup; 2 (the default) also in launches whose
 //                          groups merge parts (see plan_decode)
 struct Knobs {
+  int stream_min = 0;  // AUTO: streaming kernel from this many sub-tiles per wave (0: never)
   int kpg = 0;
   int early = 1;
   int solo = 1;
@@ -178,7 +179,38 @@ struct DecodePlan {
   bool dyn = false;     // dynamic sub-tile claims
   bool long_waves = false;  // every wave streams 4 or more sub-tiles on average
   bool mf = false;      // matrix-core kernel
+  bool stream = false;  // the streaming kernel (decode_stream.hip)
 };
+
+// The streaming kernel's plan: groups of up to 8 heads, kpg parts per group
+// sized so that the launch has about one workgroup per CU (each part at least
+// one sub-tile). Returns false where the kernel does not apply.
+constexpr int kStreamWaves = 8;
+bool plan_stream(DecodePlan& p, mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep, int head_dim) {
+  if (head_dim != 64 && head_dim != 128) return false;
+  p = DecodePlan{};
+  p.group = mi::decode_group_size(n_rep);
+  p.n_chunks = n_rep / p.group;
+  const int gpi = n_head_kv * p.n_chunks;
+  int64_t sub = 0;
+  for (int i = 0; i < n_items; ++i) {
+    it[i].spg = (it[i].n_kv + mi::kDecodeSub - 1) / mi::kDecodeSub;
+    sub += (int64_t)gpi * it[i].spg;
+  }
+  int64_t wg = 0;
+  for (int i = 0; i < n_items; ++i) {
+    int64_t k = g.knobs.kpg > 0 ? g.knobs.kpg : (int64_t)g.n_cu * it[i].spg / std::max<int64_t>(1, sub);
+    k = std::max<int64_t>(1, std::min<int64_t>(k, it[i].spg));
+    it[i].kpg = (int32_t)k;
+    it[i].wg0 = (int32_t)wg;
+    wg += (int64_t)gpi * k;
+    p.grid_x = std::max<int>(p.grid_x, gpi * (int)k);
+  }
+  p.n_wg = (int)wg;
+  p.long_waves = sub >= (int64_t)g.knobs.stream_min * wg * kStreamWaves;
+  p.stream = true;
+  return true;
+}
 
 // Assigns kpg and the first record of every item for gpi groups per item.
 // pos_bytes: one position's K and V row bytes.
@@ -564,7 +596,17 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
         return fail(MI_HIP_E_UNSUPPORTED,
                     "item %d: n_kv * position stride exceeds 2^31 bytes for one KV head", base + cnt);
     }
-    plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16, ws->groups);
+    const int dmode = g.decode_mode.load();
+    bool streamed = false;
+    if (dmode == MI_HIP_DECODE_STREAM || (dmode == MI_HIP_DECODE_AUTO && g.knobs.stream_min > 0 && !r0.f16)) {
+      DecodePlan sp;
+      if (plan_stream(sp, p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim) &&
+          (dmode == MI_HIP_DECODE_STREAM || sp.long_waves)) {
+        plan = sp;
+        streamed = true;
+      }
+    }
+    if (!streamed) plan = plan_decode(p.item, cnt, r0.n_head_kv, items[0].n_rep, r0.head_dim, r0.f16, ws->groups);
     const int gpi = r0.n_head_kv * plan.n_chunks;
     const int team = mi::decode_team(r0.head_dim, r0.f16, plan.group);
     for (int i = 0; i < cnt; ++i)
@@ -589,6 +631,7 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
     p.status = ws->status;
     p.ctr_groups = ws->groups;
     p.max_polls = ws->max_polls;
+    p.rec_words = (int32_t)(mi::decode_record_floats(r0.head_dim, plan.group) / 2);
     p.det = g.deterministic.load();
     // The early merge is worth its wait when every workgroup of the launch can
     // be resident at once (one per CU); it stays correct otherwise.
@@ -606,7 +649,9 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
     if (launches > 1 && (rc = plan_launch(base, p, cnt, plan))) return rc;
     if ((rc = ws_next_epoch(ws, cnt * p.gpi, stream, &p.epoch, &p.clear_groups))) return rc;
     hipError_t e =
-        mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, plan.mf, stream);
+        plan.stream
+            ? mi::launch_stream_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, stream)
+            : mi::launch_decode(p, plan.grid_x, cnt, r0.head_dim, r0.f16, plan.group, plan.dyn, plan.mf, stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
   }
   return MI_HIP_OK;
@@ -835,6 +880,7 @@ int mi_hip_init(int device) {
   g.knobs.solo = env_int("MI_HIP_DECODE_SOLO", 1);
   g.knobs.claim = env_int("MI_HIP_DECODE_CLAIM", 0);
   g.knobs.hsplit = env_int("MI_HIP_DECODE_HSPLIT", 2);
+  g.knobs.stream_min = env_int("MI_HIP_DECODE_STREAM_MIN", 0);
   g.ready = true;
   // The default workspace: head_dim up to 128, groups of up to 8 heads, up to
   // 1024 groups per launch (e.g. 32 items x 32 KV heads), ~11 MB.
@@ -1064,8 +1110,10 @@ int mi_hip_set_prefill_mode(int32_t mode) {
 }
 
 int mi_hip_set_decode_mode(int32_t mode) {
-  if (mode != MI_HIP_DECODE_VALU && mode != MI_HIP_DECODE_MATRIX && mode != MI_HIP_DECODE_AUTO)
-    return fail(MI_HIP_E_INVALID, "decode mode %d: MI_HIP_DECODE_VALU (0), _MATRIX (1) or _AUTO (2)", mode);
+  if (mode != MI_HIP_DECODE_VALU && mode != MI_HIP_DECODE_MATRIX && mode != MI_HIP_DECODE_AUTO &&
+      mode != MI_HIP_DECODE_STREAM)
+    return fail(MI_HIP_E_INVALID, "decode mode %d: MI_HIP_DECODE_VALU (0), _MATRIX (1), _AUTO (2) or _STREAM (3)",
+                mode);
   g.decode_mode.store(mode);
   return MI_HIP_OK;
 }

@@ -33,6 +33,7 @@ MI_HIP_PREFILL_SPLIT_BF16 = 1
 MI_HIP_DECODE_VALU = 0
 MI_HIP_DECODE_MATRIX = 1
 MI_HIP_DECODE_AUTO = 2
+MI_HIP_DECODE_STREAM = 3
 
 MI_HIP_QWEN2_ATTN_FUSED = 0
 MI_HIP_QWEN2_ATTN_REFERENCE_ORDER = 1

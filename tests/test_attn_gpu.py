@@ -126,7 +126,8 @@ def test_decode_f16_cache_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv, decod
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
 
 
-@pytest.fixture(params=[mh.MI_HIP_DECODE_MATRIX, mh.MI_HIP_DECODE_VALU], ids=["matrix", "valu"])
+@pytest.fixture(params=[mh.MI_HIP_DECODE_MATRIX, mh.MI_HIP_DECODE_VALU, mh.MI_HIP_DECODE_STREAM],
+                ids=["matrix", "valu", "stream"])
 def decode_mode(request, hip):
     """Runs a decode test on each decode kernel (matrix cores, vector units);
     the library default picks one of them per launch."""

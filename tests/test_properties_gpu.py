@@ -28,7 +28,8 @@ H, HKV, D = 14, 2, 64
 SCALE = D ** -0.5
 
 
-@pytest.fixture(params=[mh.MI_HIP_DECODE_MATRIX, mh.MI_HIP_DECODE_VALU], ids=["matrix", "valu"])
+@pytest.fixture(params=[mh.MI_HIP_DECODE_MATRIX, mh.MI_HIP_DECODE_VALU, mh.MI_HIP_DECODE_STREAM],
+                ids=["matrix", "valu", "stream"])
 def kernel(request, hip):
     hip.check(hip.mi_hip_set_decode_mode(request.param))
     yield request.param
