@@ -59,12 +59,34 @@ def causal_flops(n, h, d):
     return 4 * d * h * n * (n + 1) // 2
 
 
+SPINUP_S = 0.03
+
+
+def spin_up(torch, launch, seconds=SPINUP_S):
+    """Untimed launches of the same step for `seconds` of wall time before a
+    measurement: the GPU's clock ramps over the first ~15-20 ms of continuous
+    work after an idle gap (measured: prefill-1024 blocks of 220 launches ran
+    26.8, 25.7, 24.8, then 24.3 us per launch steadily), and every measurement
+    here follows host-side setup that leaves the device idle."""
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        for _ in range(64):
+            launch(i)
+            i += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 def run_timed(torch, launch, steps, warmup):
-    """warmup untimed steps, then `steps` timed steps back to back, bracketed by
-    synchronize and by two HIP events on the stream the kernels run on; returns
-    ms per step. (Events between the launches would put their own commands
-    between the kernels, so the per-launch time of a one-launch step is this
-    same figure; rocprofv3 gives the kernel's own duration.)"""
+    """A clock spin-up (spin_up), warmup untimed steps, then `steps` timed steps
+    back to back, bracketed by synchronize and by two HIP events on the stream
+    the kernels run on; returns ms per step. (Events between the launches would
+    put their own commands between the kernels, so the per-launch time of a
+    one-launch step is this same figure; rocprofv3 gives the kernel's own
+    duration.)"""
+    spin_up(torch, launch)
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
@@ -670,6 +692,7 @@ def main():
             "workload": "decode attention: 24 independent layer caches x n_kv=4096, 1 query "
                         "token, 14 Q / 2 KV heads (GQA 7), head_dim 64, F32 K/V, one batched "
                         "launch per step, cache sets rotated beyond the 256 MB MALL",
+            "spinup_s": SPINUP_S,
             "n_layers": 24, "n_kv": 4096, "n_head": 14, "n_head_kv": 2, "head_dim": 64,
             "cache_sets": d["sets"] if d else None,
         },

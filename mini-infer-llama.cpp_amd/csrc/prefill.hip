@@ -1,5 +1,7 @@
 // prefill.hip -- fused causal ATTN_QK -> SOFTMAX -> ATTN_KQV for n_tokens > 1
-// queries (src/ops_cpu.cpp:304-410), on the FP32 matrix cores of gfx950.
+// queries (src/ops_cpu.cpp:304-410) on the matrix cores of gfx950: float
+// products on v_mfma_f32_32x32x2f32 (the default), or an opt-in form whose
+// float operands are split into bf16 pairs for v_mfma_f32_32x32x16_bf16.
 //
 // Work decomposition. A query block is 32 consecutive queries of one head; it
 // sees ceil((n_past + 32 (i + 1)) / 32) key tiles of 32 keys (causal). One
@@ -17,22 +19,26 @@
 //      ... lds (no registers), four rows per instruction, 16-byte slots XOR-
 //      swizzled by row; lane (c, kh) then reads K[key c][kh D/2 ..] from it,
 //      conflict-free, as the A operand. V goes straight to registers in the
-//      A layout of the PV product (lane (c, kh) holds V[key][dim c + 32 db]
-//      for the 16 keys 8(t/4) + 4kh + t%4: one 128-byte row piece per
-//      half-wave and load);
+//      A layout of the PV product: lane (c, kh) holds V[key][NDB c + db] for
+//      the 16 keys 8(t/4) + 4kh + t%4, one load of NDB = D/32 consecutive
+//      elements per key (so row c of output block db is dim NDB c + db);
 //   2. S^T = K . Q^T with D/2 v_mfma_f32_32x32x2f32: B = the block's queries,
 //      pre-scaled by scale*log2(e) (staged once per workgroup in LDS at
 //      head_dim 64);
-//   3. causal mask (key > n_past + query) and online softmax in base 2: a lane
-//      holds 16 keys of query c and its partner lane (lane ^ 32) the other 16
-//      (one permlane32 swap combines them);
+//   3. causal mask (key > n_past + query; only on tiles that reach past a
+//      query of the block) and online softmax in base 2: a lane holds 16 keys
+//      of query c and its partner lane (lane ^ 32) the other 16 (one
+//      permlane32 swap combines them); O is rescaled only when some row's
+//      maximum moved;
 //   4. O^T += V^T . P^T with 16 MFMAs per 32 output dims; S^T leaves step 3 in
 //      the B-operand layout of this product (register r of a lane = key
 //      8(r/4) + 4kh + r%4), so P needs no shuffle.
 // The units are software-pipelined: while unit u's softmax runs on the vector
-// ALUs, the next unit's QK products run on the matrix cores; the K tile after
-// that is requested as soon as the LDS tile has been read, V after the PV
-// products that consumed the previous one.
+// ALUs, the next unit's QK products run on the matrix cores (the two are
+// interleaved instruction by instruction: the products form one dependent
+// chain, which would otherwise hold the wave's issue until it drains); the K
+// tile after that is requested as soon as the LDS tile has been read, V after
+// the PV products that consumed the previous one.
 // At the end the waves' (m, l, O) records meet in LDS and each block's output
 // is merged with the stable rescaling; nothing else leaves the workgroup. Two
 // waves per SIMD at head_dim 64 (one at 128) let one wave's vector work run
@@ -43,6 +49,9 @@
 namespace mi {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -124,6 +133,7 @@ struct PrefillCfg {
   static constexpr int HALF = D / 2;                   // QK MFMA steps
   static constexpr int NDB = D / 32;                   // PV output blocks of 32 dims
   static constexpr int NV = 16 * NDB;                  // V values per lane per tile
+  static constexpr int NVL = 16;                       // V loads per lane per tile (one per key)
   static constexpr int RB = D * ELT;                   // bytes per K row
   static constexpr int NSLOT = RB / 16;                // 16-byte slots per K row
   static constexpr int KTILE = kPrefillKeys * RB;      // bytes of one K tile
@@ -143,8 +153,8 @@ struct PrefillCfg {
   static constexpr int L_CTR = L_Q + (QLDS ? 2 * kPrefillRows * QRS * 4 : 0);
   static constexpr int LDS = L_CTR + 16;
   // vector memory operations a wave issues after a K tile request and before
-  // the next tile's wait (the V loads of one unit), capped at the counter's range
-  static constexpr int WAIT_K = NV < 63 ? NV : 63;
+  // the next tile's wait (the V loads of one unit)
+  static constexpr int WAIT_K = NVL;
   static_assert(KTILE % 1024 == 0, "1 KB load granularity");
   static_assert(REG % 16 == 0 && RECB % 16 == 0, "16-byte alignment");
   static_assert(LDS <= 160 * 1024, "LDS budget");
@@ -223,8 +233,12 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       }
     }
   };
-  // A operand of PV for key tile kt (rows past n_kv are zero, as for K).
-  const unsigned vvo = (unsigned)(4 * kh * vs2 + col * ELT);
+  // A operand of PV for key tile kt (rows past n_kv are zero, as for K):
+  // lane (col, kh) holds V[key][NDB col + db] for the 16 keys 8 (t / 4) +
+  // 4 kh + t % 4, one load of NDB consecutive elements per key. Output block
+  // db's row c is therefore dim NDB c + db (write_record puts dims back in
+  // order).
+  const unsigned vvo = (unsigned)(4 * kh * vs2 + col * NDB * ELT);
   auto load_v = [&](int kt, float (&vv)[NV]) __attribute__((always_inline)) {
     const int key0 = kt * kPrefillKeys;
     const unsigned to_lane = key0 + kPrefillKeys <= n_kv ? 0u : ~0u;
@@ -232,8 +246,23 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     for (int t = 0; t < 16; ++t) {
       const unsigned row = (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
       const unsigned vo = vvo + (row & to_lane), so = row & ~to_lane;
+      if constexpr (ELT == 4 && NDB == 2) {
+        const f32x2 x = __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(vr, vo, so, 0));
+        vv[2 * t] = x[0];
+        vv[2 * t + 1] = x[1];
+      } else if constexpr (ELT == 4 && NDB == 4) {
+        const f32x4 x = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, vo, so, 0));
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) vv[t * NDB + db] = load1<KT>(vr, vo + 32 * db * ELT, so);
+        for (int db = 0; db < 4; ++db) vv[4 * t + db] = x[db];
+      } else if constexpr (ELT == 2 && NDB == 2) {
+        const f16x2 x = __builtin_bit_cast(f16x2, __builtin_amdgcn_raw_buffer_load_b32(vr, vo, so, 0));
+        vv[2 * t] = (float)x[0];
+        vv[2 * t + 1] = (float)x[1];
+      } else {
+        const f16x4 x = __builtin_bit_cast(f16x4, __builtin_amdgcn_raw_buffer_load_b64(vr, vo, so, 0));
+#pragma unroll
+        for (int db = 0; db < 4; ++db) vv[4 * t + db] = (float)x[db];
+      }
     }
   };
 
@@ -324,12 +353,14 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   auto write_record = [&](int slot) __attribute__((always_inline)) {
     lds_f32* const rec = rec_at(wave, slot);
     const float ltot = xor32_sum(lsum);
+    // register 4 r4 + i of block db holds dim NDB (8 r4 + 4 kh + i) + db
 #pragma unroll
-    for (int db = 0; db < NDB; ++db)
+    for (int r4 = 0; r4 < 4; ++r4)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4)
-        *reinterpret_cast<lds_f32x4*>(rec + col * RS + 32 * db + 8 * r4 + 4 * kh) =
-            f32x4{o[db][4 * r4 + 0], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]};
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+          rec[col * RS + NDB * (8 * r4 + 4 * kh + i) + db] = o[db][4 * r4 + i];
     if (kh == 0) {
       rec[kPrefillRows * RS + col] = m;
       rec[kPrefillRows * RS + kPrefillRows + col] = ltot;
@@ -365,31 +396,42 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     return s;
   };
 
-  // Causal mask and online softmax (base 2) of unit (block X, tile kt): s
-  // becomes the probabilities, (m, lsum, O) move on. No branches, so the
-  // compiler can interleave it with the next unit's QK products.
-  auto softmax = [&](floatx16& s, int X, int kt) __attribute__((always_inline)) {
-    const int lim = p.n_past + X * kPrefillRows + col - kt * kPrefillKeys - 4 * kh;
+  // Causal mask of unit (block X, tile kt), applied only where some key of
+  // the tile lies past some query of the block (a wave-uniform test: the
+  // diagonal tile, and tiles crossing n_kv, whose keys past n_kv are past
+  // every query).
+  auto mask = [&](floatx16& s, int X, int kt) __attribute__((always_inline)) {
+    if (p.n_past + (X - kt) * kPrefillRows < kPrefillKeys - 1) {
+      const int lim = p.n_past + X * kPrefillRows + col - kt * kPrefillKeys - 4 * kh;
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr)
-      if (8 * (rr >> 2) + (rr & 3) > lim) s[rr] = -INFINITY;
-    float mx = s[0];
-#pragma unroll
-    for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, s[rr]);
+      for (int rr = 0; rr < 16; ++rr) s[rr] = 8 * (rr >> 2) + (rr & 3) > lim ? -INFINITY : s[rr];
+    }
+  };
+  // Online softmax (base 2) of a masked unit: s becomes the probabilities,
+  // (m, lsum) move on and alpha holds O's pending rescale factor. No
+  // branches, so the next unit's QK products interleave with it.
+  float alpha = 1.f;
+  auto softmax = [&](floatx16& s) __attribute__((always_inline)) {
+    const float a0 = fmaxf(fmaxf(s[0], s[1]), s[2]), a1 = fmaxf(fmaxf(s[3], s[4]), s[5]);
+    const float a2 = fmaxf(fmaxf(s[6], s[7]), s[8]), a3 = fmaxf(fmaxf(s[9], s[10]), s[11]);
+    const float a4 = fmaxf(fmaxf(s[12], s[13]), s[14]);
+    const float mx = fmaxf(fmaxf(fmaxf(a0, a1), fmaxf(a2, a3)), fmaxf(a4, s[15]));
     const float mn = fmaxf(m, xor32_max(mx));
     const float mu = mn == -INFINITY ? 0.f : mn;
-    const float alpha = fast_exp2(m - mu);
-    float ps = 0.f;
+    alpha = fast_exp2(m - mu);
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const float e = fast_exp2(s[rr] - mu);
-      s[rr] = e;
-      ps += e;
-    }
-    lsum = lsum * alpha + ps;
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+    for (int rr = 0; rr < 16; ++rr) s[rr] = fast_exp2(s[rr] - mu);
+    const float b0 = (s[0] + s[1]) + (s[2] + s[3]), b1 = (s[4] + s[5]) + (s[6] + s[7]);
+    const float b2 = (s[8] + s[9]) + (s[10] + s[11]), b3 = (s[12] + s[13]) + (s[14] + s[15]);
+    lsum = lsum * alpha + ((b0 + b1) + (b2 + b3));
     m = mn;
+  };
+  // O's rescale, skipped when no row's maximum moved (alpha == 1 throughout)
+  auto rescale_o = [&]() __attribute__((always_inline)) {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0ull) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+    }
   };
 
   // O^T += V^T . P^T: 16 v_mfma_f32_32x32x2f32 per 32 output dims, or (SPLIT)
@@ -441,6 +483,8 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile is read before it is refilled
     if (un < T) request_k(unit_tile(un));
     __builtin_amdgcn_sched_barrier(0);
+    // (after the K request: every K request is followed by exactly NVL loads
+    // before the wait that reads its tile)
     load_v(unit_tile(u), vv);
     while (un < T) {
       // sc: scores of unit u; the LDS tile is filling with unit un's K
@@ -450,17 +494,28 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
         load_q(Xn);
         split_q();
       }
+      mask(sc, Xu, unit_tile(u));
       wait_vmem<C::WAIT_K>();
       read_k(kk);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the whole A operand at once
       __builtin_amdgcn_sched_barrier(0);
       const floatx16 sn = qk(kk);
-      softmax(sc, Xu, unit_tile(u));
+      softmax(sc);
+      if constexpr (!SPLIT) {
+        // one QK product, then a few softmax instructions, in turn (the
+        // products form a dependent chain that would otherwise stall the
+        // wave's issue, the softmax waiting behind them)
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        }
+      }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      // (unconditional, the last unit's tile past the end, so the loop body
-      // has no branch around it)
-      request_k(unit_tile(min(unn, T - 1)));
+      // no request past the wave's last unit (its region becomes a record)
+      if (unn < T) request_k(unit_tile(unn));
       __builtin_amdgcn_sched_barrier(0);
+      rescale_o();
       pv(sc, vv);
       if (Xn != Xu) {
         write_record(0);  // this wave's part of block qa
@@ -472,9 +527,11 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       un = unn;
     }
     // the last unit: no next QK to overlap
-    softmax(sc, blk(u), unit_tile(u));
+    mask(sc, blk(u), unit_tile(u));
+    softmax(sc);
+    rescale_o();
     pv(sc, vv);
-    wait_vmem<0>();  // the last tile request lands before the region becomes a record
+    wait_vmem<0>();  // every load has landed before the region becomes a record
     write_record(cur == qa ? 0 : 1);
   }
   // a wave without a block-qz record marks its region (it held a K tile)
