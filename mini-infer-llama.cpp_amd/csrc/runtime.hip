@@ -197,9 +197,15 @@ bool plan_stream(DecodePlan& p, mi::DecodeItem* it, int n_items, int n_head_kv, 
     it[i].spg = (it[i].n_kv + mi::kDecodeSub - 1) / mi::kDecodeSub;
     sub += (int64_t)gpi * it[i].spg;
   }
+  // Parts per group: about one workgroup per CU for the launch, at most
+  // kStreamMaxParts (the last part to arrive merges every record, kStreamMaxParts
+  // of them in two rounds of loads; one layer at n_kv 4096 took 63 us with 128
+  // parts against 8 us for the ring kernel), each at least 4 sub-tiles.
+  constexpr int64_t kStreamMaxParts = 16;
   int64_t wg = 0;
   for (int i = 0; i < n_items; ++i) {
     int64_t k = g.knobs.kpg > 0 ? g.knobs.kpg : (int64_t)g.n_cu * it[i].spg / std::max<int64_t>(1, sub);
+    if (g.knobs.kpg <= 0) k = std::min<int64_t>(k, std::min<int64_t>(kStreamMaxParts, it[i].spg / 4));
     k = std::max<int64_t>(1, std::min<int64_t>(k, it[i].spg));
     it[i].kpg = (int32_t)k;
     it[i].wg0 = (int32_t)wg;
