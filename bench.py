@@ -582,8 +582,8 @@ def main():
     res = {}
     if want("decode"):
         res["decode"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)
-        # the other kernels on the same workload (the default for this launch
-        # is the streaming vector-unit kernel)
+        # the other kernels on the same workload (the default for an F32 cache
+        # is the vector-unit kernel with its LDS ring)
         for key, mode in (("decode_matrix", mh.MI_HIP_DECODE_MATRIX), ("decode_stream", mh.MI_HIP_DECODE_STREAM)):
             lib.check(lib.mi_hip_set_decode_mode(mode))
             res[key] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup)

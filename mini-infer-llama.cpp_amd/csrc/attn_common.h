@@ -160,6 +160,13 @@ __device__ __forceinline__ void lds_store(lds_t* p, T v) {
 __device__ inline void dma16(rsrc_t r, lds_t* lds, unsigned voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, 0);
 }
+// Cache-policy bit of a buffer access (gfx950 cpol): nontemporal, for data
+// read once per launch (a KV cache stream), so that it does not displace what
+// the caches hold for longer.
+constexpr int kNt = 2;
+__device__ inline void dma16_nt(rsrc_t r, lds_t* lds, unsigned voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, voff, 0, 0, kNt);
+}
 
 // LDS rows of NSLOT 16-byte slots: logical slot j of row r is stored at
 // physical slot j ^ swz(r), so 16 lanes reading one slot of 16 consecutive

@@ -462,9 +462,9 @@ void decode_kernel(const DecodeParams p) {
       rows[SL] = r0;
     }
 #pragma unroll
-    for (int i = 0; i < C::NDK; ++i) dma16(kr, slot + 1024 * i, offk[i]);
+    for (int i = 0; i < C::NDK; ++i) dma16_nt(kr, slot + 1024 * i, offk[i]);
 #pragma unroll
-    for (int i = 0; i < C::NDK; ++i) dma16(vr, slot + C::SUBB + 1024 * i, offv[i]);
+    for (int i = 0; i < C::NDK; ++i) dma16_nt(vr, slot + C::SUBB + 1024 * i, offv[i]);
   };
   // Dynamic takes: pend[s] is the claim (issued by lane 0 one ring cycle ago)
   // that names slot s's next sub-tile, nst + claim, after the fixed prefix of

@@ -8,32 +8,36 @@
 // per_wg) of the buffer; each thread keeps 8 loads of 16 bytes in flight
 // (consecutive threads read consecutive pieces, so every load instruction of
 // a wave covers 1 KB of contiguous memory) and the workgroup writes one float.
+// The loads are nontemporal, as the decode kernels' cache streams are: data
+// read once does not displace what the caches hold (on the 100.7 MB cache
+// read of 24 layers x n_kv 4096 this is worth about 2 us of 18).
 #include "kernels.h"
 #include "mi_hip_attn.h"
 
 namespace mi {
 
 constexpr int kMemreadThreads = 512;
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kMemreadUnroll = 8;
 
-__global__ __launch_bounds__(kMemreadThreads) void memread_kernel(const float4* src, int64_t n4,
+__global__ __launch_bounds__(kMemreadThreads) void memread_kernel(const f32x4_t* src, int64_t n4,
                                                                  int64_t per_wg, float* sums) {
   const int64_t b0 = (int64_t)blockIdx.x * per_wg;
   const int64_t b1 = min(b0 + per_wg, n4);
   constexpr int64_t step = kMemreadThreads;
-  float4 acc[kMemreadUnroll];
+  f32x4_t acc[kMemreadUnroll];
 #pragma unroll
-  for (int u = 0; u < kMemreadUnroll; ++u) acc[u] = float4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < kMemreadUnroll; ++u) acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   int64_t i = b0 + threadIdx.x;
   // every piece read here is below b1 <= n4
   for (; i + (kMemreadUnroll - 1) * step < b1; i += kMemreadUnroll * step) {
-    float4 v[kMemreadUnroll];
+    f32x4_t v[kMemreadUnroll];
 #pragma unroll
-    for (int u = 0; u < kMemreadUnroll; ++u) v[u] = src[i + u * step];
+    for (int u = 0; u < kMemreadUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * step);
 #pragma unroll
     for (int u = 0; u < kMemreadUnroll; ++u) acc[u] += v[u];
   }
-  for (; i < b1; i += step) acc[0] += src[i];
+  for (; i < b1; i += step) acc[0] += __builtin_nontemporal_load(src + i);
   float s = 0.f;
 #pragma unroll
   for (int u = 0; u < kMemreadUnroll; ++u) s += (acc[u].x + acc[u].y) + (acc[u].z + acc[u].w);
@@ -52,7 +56,7 @@ hipError_t launch_memread(const void* src, size_t bytes, float* sums, int n_sums
   const int64_t n4 = (int64_t)(bytes / 16);
   const int64_t per_wg = (n4 + n_sums - 1) / n_sums;
   hipLaunchKernelGGL(memread_kernel, dim3((unsigned)n_sums), dim3(kMemreadThreads), 0, stream,
-                     static_cast<const float4*>(src), n4, per_wg, sums);
+                     static_cast<const f32x4_t*>(src), n4, per_wg, sums);
   return hipGetLastError();
 }
 
