@@ -539,16 +539,16 @@ def cpu_baseline(n_layers_sample=24, n_kv=4096, target_s=12.0):
 
 def measured_mfma():
     """Matrix-core use of the prefill kernel from the committed rocprofv3
-    counter summary (profiles/prefill_mfma.txt): split bf16 pairs at n=1024
-    and 4096, float products at n=1024."""
+    counter summary (profiles/prefill_mfma.txt): float products at n=1024
+    and 4096, split bf16 pairs at n=1024."""
     p = os.path.join(ROOT, "profiles", "prefill_mfma.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
         m = json.load(f)
-    keep = ("kernel_us", "mfma_insts", "issued_tflops", "issued_peak_tflops", "issued_frac_of_peak",
-            "mfma_busy_frac", "causal_frac_of_fp32_peak")
-    return {"source": "profiles/prefill_mfma.txt (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_BF16/_F32, "
+    keep = ("kernel_us", "mfma_insts", "issued_flops", "issued_tflops", "issued_peak_tflops", "issued_frac_of_peak",
+            "mfma_busy_frac", "causal_frac_of_issued_peak")
+    return {"source": "profiles/prefill_mfma.txt (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F32/_BF16, "
                       "kernel trace)",
             **{k: {f: v[f] for f in keep if f in v} for k, v in m.items()}}
 
@@ -720,8 +720,8 @@ def main():
         if "read_floor" in res:
             rf = res["read_floor"]
             out["roofline"]["read_floor"] = {
-                "what": "mi_hip_memread over exactly the step's 100,663,296 cache bytes, 7 buffers rotated, "
-                        "back to back; fastest workgroup count",
+                "what": "mi_hip_memread (nontemporal 16-byte loads, as the decode kernel's) over exactly the "
+                        "step's 100,663,296 cache bytes, 7 buffers rotated, back to back; fastest workgroup count",
                 "us": round(rf["us"], 3), "gbps": round(rf["gbps"], 1),
                 "frac_of_peak": round(rf["gbps"] / HBM_PEAK_GBPS, 4), "workgroups": rf["workgroups"],
                 "us_by_workgroups": rf["us_by_workgroups"],
@@ -750,6 +750,11 @@ def main():
         }
     if "prefill1024" in res:
         p1, p4 = res["prefill1024"], res["prefill4096"]
+        mm = measured_mfma()
+        # FLOPs the launch issues on the matrix cores (the causal count plus the
+        # diagonal tiles' masked halves), from the instruction counters; the
+        # same in every launch of this shape
+        issued = (mm or {}).get("f32_1024", {}).get("issued_flops")
         out["prefill"] = {
             "metric": "prefill-1024 causal attn TFLOP/s (14 Q / 2 KV heads, head_dim 64, F32)",
             "products": "f32 (v_mfma_f32_32x32x2f32, the issued type)",
@@ -758,7 +763,12 @@ def main():
             "roofline": {"bound": "mfma", "achieved": round(p1["tflops"], 2),
                          "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(p1["tflops"] / FP32_MFMA_PEAK_TFLOPS, 4),
-                         "flops_per_launch": p1["flops"], "mfma_counters": measured_mfma()},
+                         "flops_per_launch": p1["flops"],
+                         "issued_flops_per_launch": issued,
+                         "issued_tflops": round(issued / p1["kernel_ms"] / 1e9, 2) if issued else None,
+                         "issued_frac": (round(issued / p1["kernel_ms"] / 1e9 / FP32_MFMA_PEAK_TFLOPS, 4)
+                                         if issued else None),
+                         "mfma_counters": mm},
         }
         if "prefill1024_split" in res:
             ps = res["prefill1024_split"]

@@ -294,6 +294,14 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
       plan_items(q, it, n_items, n_head_kv * q.n_chunks, waves, ring, pos_bytes);
       bool keep = true;
       for (int i = 0; i < n_items; ++i) keep = keep && it[i].kpg >= kpg0[i];
+      // An F16 cache takes the split (vector units) only where the split
+      // launch's waves stream fewer than 4 sub-tiles each on average; longer
+      // streams run faster whole on the matrix cores. One layer, F16, with the
+      // split's sub-tiles per wave: 28/4 heads, D 128 at n_kv 8192 (4) 10.7
+      // against 14.5 us split; 14/2 heads, D 64 at 32768 (4) 11.9 against
+      // 14.3; at 8192 (2) 9.5 against 9.6; at 1024-4096 (1) 7.9-8.0 against
+      // 9.0-9.1 split; 28/4 heads at 512 (1) 8.8 against 10.5 split.
+      if (autom && f16 && q.long_waves) keep = false;
       if (keep) {
         q.mf = p.mf;  // sub-tiles and workgroups both double: long_waves stands
         p = q;
@@ -304,9 +312,8 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
     }
   }
   // An F16 cache runs on the vector units only where its heads were split
-  // (one layer of the 0.5B shape, n_kv 256-8192: 6.5-9.1 us against 6.8-9.6
-  // with the matrix products, which win at 512, 16384, for 24 layers and for
-  // the 7B shape at n_kv 4096 and 8192, where the split does not apply).
+  // (above); otherwise on the matrix cores (24 layers of 14/2 heads at n_kv
+  // 4096: 15.8 against 20.8 us).
   if (autom && f16 && !split) p.mf = true;
   return p;
 }
