@@ -174,8 +174,10 @@ int mi_hip_set_prefill_mode(int32_t mode);
  *     merged by the last to arrive), for head_dim 64 or 128 and groups that
  *     span several workgroups; other launches take MI_HIP_DECODE_VALU.
  *   MI_HIP_DECODE_AUTO (the default): the vector units (MI_HIP_DECODE_VALU)
- *     for an F32 cache; for an F16 cache the matrix cores unless the launch's
- *     heads are split between workgroups (a vector-unit form).
+ *     for an F32 cache; for an F16 cache the matrix cores, except for short
+ *     launches whose heads can be split between workgroups so that each
+ *     wave streams fewer than 4 sub-tiles of 16 positions (the split is a
+ *     vector-unit form, faster there).
  * The split bf16 pairs of the matrix form carry ~2^-16 relative error per
  * product into the scores, so with an F32 cache it stays within the 1e-4 bar
  * only while scale * |q| * |k| stays small (N(0,1) inputs with q and k
@@ -277,12 +279,17 @@ int mi_hip_attn_fwd(const mi_hip_attn_args* args);
 /* n_items independent single-token decode problems of one shape (same
  * head_dim, n_head, n_rep, K/V element type; n_past may differ) in ONE
  * launch, e.g. many sequences' caches, or a stack of layers in a benchmark.
- * No counterpart in the reference (it runs one node per layer). */
+ * No counterpart in the reference (it runs one node per layer).
+ * Decode launches take a fresh stamp on their workspace from the host at
+ * every call, so a call on a stream under graph capture is refused with
+ * MI_HIP_E_UNSUPPORTED (a replayed launch would reuse its stamp); the same
+ * holds for every decode entry point. */
 int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* stream);
 
 /* mi_hip_attn_decode_batch for callers that cannot allocate device memory
- * (code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc). No counterpart in the reference. It ignores the items' ws and
+ * (tight serving loops, harnesses that forbid hipMalloc). No counterpart in
+ * the reference. Like every decode entry point it is refused on a stream
+ * under graph capture. It ignores the items' ws and
  * their caches' workspaces and uses a fixed 4 MB scratch array that each GPU
  * holds from library load until the process ends (at most 128 groups, i.e.
  * items x n_head_kv x head chunks, and records for ~460-900 workgroups); a
