@@ -276,6 +276,19 @@ typedef struct mi_hip_attn_args {
  * within floating-point tolerance. */
 int mi_hip_attn_fwd(const mi_hip_attn_args* args);
 
+/* The same triple in the reference's own operation order, so that the output
+ * equals mi_compute_attn_qk -> mi_compute_softmax -> mi_compute_attn_kqv
+ * (src/ops_cpu.cpp:304-410) on the nodes of src/model_qwen2.cpp:169-172 BIT
+ * FOR BIT, not within tolerance: each score's dot product d ascending with
+ * every product and sum rounded, the maximum, the host C library's expf, the
+ * sum of the exponentials key by key, the correctly rounded 1 / sum, and each
+ * output element's sum over the keys in order. The device engine's
+ * MI_HIP_QWEN2_ATTN_REFERENCE_ORDER mode runs it. F32 cache only, head_dim 64
+ * or 128, n_past + n_tokens <= 32768 (MI_HIP_E_UNSUPPORTED otherwise). The
+ * ordered sums make a row's cost linear in its key count on one lane: a
+ * parity path, slower than mi_hip_attn_fwd. */
+int mi_hip_attn_fwd_reference_order(const mi_hip_attn_args* args);
+
 /* n_items independent single-token decode problems of one shape (same
  * head_dim, n_head, n_rep, K/V element type; n_past may differ) in ONE
  * launch, e.g. many sequences' caches, or a stack of layers in a benchmark.

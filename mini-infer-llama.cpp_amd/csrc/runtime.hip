@@ -1257,6 +1257,43 @@ int mi_hip_attn_fwd(const mi_hip_attn_args* a) {
   return a->n_tokens == 1 ? run_decode(a, 1, st, workspace_of(a)) : run_prefill(a, r, st);
 }
 
+int mi_hip_attn_fwd_reference_order(const mi_hip_attn_args* a) {
+  if (!a) return fail(MI_HIP_E_INVALID, "args is NULL");
+  Resolved r;
+  int rc = resolve_kv(a, &r);
+  if (rc) return rc;
+  if ((rc = check_problem(a, r))) return rc;
+  if (r.f16) return fail(MI_HIP_E_UNSUPPORTED, "reference-order attention reads an F32 cache (the reference's)");
+  const int64_t n_kv = (int64_t)a->n_past + a->n_tokens;
+  if (n_kv > mi::kExactMaxKeys)
+    return fail(MI_HIP_E_UNSUPPORTED, "reference-order attention covers up to %d keys", mi::kExactMaxKeys);
+  // a KV head's V rows are addressed with 32-bit byte offsets
+  if (n_kv * r.v_s2 + 4LL * r.head_dim > INT32_MAX)
+    return fail(MI_HIP_E_UNSUPPORTED, "n_kv * position stride exceeds 2^31 bytes for one KV head");
+  if ((rc = bind_device())) return rc;
+  mi::ExactAttn ea{};
+  ea.q = reinterpret_cast<const char*>(a->q);
+  ea.k = r.k;
+  ea.v = r.v;
+  ea.out = reinterpret_cast<char*>(a->out);
+  ea.q_s1 = (int64_t)a->q_nb[1];
+  ea.q_s2 = (int64_t)a->q_nb[2];
+  ea.k_s1 = r.k_s1;
+  ea.k_s2 = r.k_s2;
+  ea.v_s1 = r.v_s1;
+  ea.v_s2 = r.v_s2;
+  ea.o_s1 = (int64_t)a->out_nb[1];
+  ea.o_s2 = (int64_t)a->out_nb[2];
+  ea.n_head = a->n_head;
+  ea.n_rep = a->n_rep;
+  ea.n_past = a->n_past;
+  ea.n_tokens = a->n_tokens;
+  ea.head_dim = r.head_dim;
+  ea.scale = a->scale;
+  const hipError_t e = mi::launch_attn_exact(ea, static_cast<hipStream_t>(a->stream));
+  return e == hipSuccess ? MI_HIP_OK : hip_fail(e, "reference-order attention launch");
+}
+
 int mi_hip_attn_decode_batch(const mi_hip_attn_args* items, int n_items, void* stream) {
   if (!items || n_items <= 0) return fail(MI_HIP_E_INVALID, "need at least one item");
   Resolved r0;

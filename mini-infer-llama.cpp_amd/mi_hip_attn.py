@@ -184,6 +184,7 @@ SIGNATURES = {
     "mi_hip_kv_write": ([_P, _I, _I, _I, _I, _P, ctypes.POINTER(ctypes.c_size_t), _I, _P], _I),
     "mi_hip_kv_bind": ([_P, _I, _I, ctypes.POINTER(MiTensor)], _I),
     "mi_hip_attn_fwd": ([ctypes.POINTER(AttnArgs)], _I),
+    "mi_hip_attn_fwd_reference_order": ([ctypes.POINTER(AttnArgs)], _I),
     "mi_hip_attn_decode_batch": ([ctypes.POINTER(AttnArgs), _I, _P], _I),
     "mi_hip_attn_decode_batch_noalloc": ([ctypes.POINTER(AttnArgs), _I, _P], _I),
     "mi_hip_op_attn_qk": ([ctypes.POINTER(MiTensor), _P], _I),
