@@ -143,7 +143,11 @@ __device__ __forceinline__ float exact_sum(const float* p, int n) {
 
 // acc + v[0] * p[0] + v[D] * p[1] + ... + v[(n - 1) D] * p[n - 1], each
 // product and sum rounded (v: one output element's column of V rows D floats
-// apart; 16 rows and probabilities readable past n)
+// apart; 16 rows and probabilities readable past n). The products do not
+// depend on the running sum: chunk c + 1's 16 are formed between chunk c's
+// additions, so each addition waits only for the one before it, not for a
+// multiplication issued just before it. (The same products, added in the
+// same order: the same bits.)
 template <int D>
 __device__ __forceinline__ float exact_dot(const float* v, const float* p, int n) {
 #pragma clang fp contract(off)
@@ -151,41 +155,78 @@ __device__ __forceinline__ float exact_dot(const float* v, const float* p, int n
   float acc = 0.0f;
   float va[16], vb[16];
   float4 pa[4], pb[4];
+  float ra[16], rb[16];  // products
   auto get = [&](float (&vv)[16], float4 (&pp)[4], int c) {
 #pragma unroll
     for (int u = 0; u < 16; ++u) vv[u] = v[(16 * c + u) * D];
 #pragma unroll
     for (int u = 0; u < 4; ++u) pp[u] = p4[4 * c + u];
   };
-  auto mac = [&](const float (&vv)[16], const float4 (&pp)[4]) {
+  auto prod = [&](float (&r)[16], const float (&vv)[16], const float4 (&pp)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      acc = acc + vv[4 * u] * pp[u].x;
-      acc = acc + vv[4 * u + 1] * pp[u].y;
-      acc = acc + vv[4 * u + 2] * pp[u].z;
-      acc = acc + vv[4 * u + 3] * pp[u].w;
+      r[4 * u] = vv[4 * u] * pp[u].x;
+      r[4 * u + 1] = vv[4 * u + 1] * pp[u].y;
+      r[4 * u + 2] = vv[4 * u + 2] * pp[u].z;
+      r[4 * u + 3] = vv[4 * u + 3] * pp[u].w;
     }
   };
+  // chunk r's additions, chunk (vv, pp)'s products into rn between them
+  auto add_prod = [&](const float (&r)[16], float (&rn)[16], const float (&vv)[16], const float4 (&pp)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc = acc + r[4 * u];
+      rn[4 * u] = vv[4 * u] * pp[u].x;
+      acc = acc + r[4 * u + 1];
+      rn[4 * u + 1] = vv[4 * u + 1] * pp[u].y;
+      acc = acc + r[4 * u + 2];
+      rn[4 * u + 2] = vv[4 * u + 2] * pp[u].z;
+      acc = acc + r[4 * u + 3];
+      rn[4 * u + 3] = vv[4 * u + 3] * pp[u].w;
+    }
+  };
+  auto add = [&](const float (&r)[16]) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) acc = acc + r[t];
+  };
   const int nch = n >> 4;
-  get(va, pa, 0);
-  int c = 0;
-  for (; c + 1 < nch; c += 2) {
-    get(vb, pb, c + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    mac(va, pa);
-    get(va, pa, c + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    mac(vb, pb);
+  if (nch > 0) {
+    get(va, pa, 0);
+    prod(ra, va, pa);
+    if (nch > 1) get(vb, pb, 1);
+    int c = 0;
+    // ra: chunk c's products; vb, pb: chunk c + 1's values
+    for (; c + 2 < nch; c += 2) {
+      get(va, pa, c + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      add_prod(ra, rb, vb, pb);
+      get(vb, pb, c + 3);  // (c + 3 <= nch: at most the chunk past the last whole one)
+      __builtin_amdgcn_sched_barrier(0);
+      add_prod(rb, ra, va, pa);
+    }
+    if (c + 1 < nch) {
+      add_prod(ra, rb, vb, pb);
+      add(rb);
+    } else {
+      add(ra);
+    }
   }
-  if (c < nch) mac(va, pa);
   for (int t = 16 * nch; t < n; ++t) acc = acc + v[t * D] * p[t];
   return acc;
 }
 
-// D: head_dim (64 or 128), so that a key's row loads are all issued at once.
+// D: head_dim (64 or 128). The row's K rows come into LDS first, into the
+// region that later holds its V rows: LDS-direct requests of whole 1 KB
+// (where a thread loading its own key row touches one cache line per lane
+// and instruction), 16-byte slots XOR-swizzled by row so that one row per
+// lane reads free of bank conflicts. After the scores, waves 1-3 bring the V
+// rows over the K rows while wave 0 forms the maximum, the exponentials and
+// the ordered sum; the barriers do not wait for vector memory (wg_barrier),
+// each wave waits for its own requests.
 template <int D>
 __global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const ExactAttn p) {
 #pragma clang fp contract(off)
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
   extern __shared__ __attribute__((aligned(16))) char ex_lds[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -195,43 +236,51 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const 
   const int a = min(p.n_past + j + 1, p.n_past + p.n_tokens);
   const int n_kv = p.n_past + p.n_tokens;
   const int vbytes = exact_staged_vbytes(n_kv, D);
-  float* const vl = reinterpret_cast<float*>(ex_lds);  // V row t at vl + t D
+  constexpr int PPR = D / 4;  // 16-byte pieces per row
+  float* const vl = reinterpret_cast<float*>(ex_lds);  // K, later V, row t at vl + t D
   float* const prob = reinterpret_cast<float*>(ex_lds + vbytes);
   uint64_t* const tab = reinterpret_cast<uint64_t*>(ex_lds + vbytes + 4 * n_kv);
   float* const red = reinterpret_cast<float*>(tab + 32);
   const uint64_t te = kExpfTab[lane & 31];  // requested first: loads complete in order
-  // the row's V rows into LDS: piece i (16 bytes) is row i / (D / 4), bytes
-  // 16 (i % (D / 4)); pieces past the row arrive as zeros. The keys' loads
-  // below complete behind these requests (in order), so V has landed before
-  // the scores are formed, and nothing after them waits on memory.
-  {
-    const char* const vbase = p.v + kvh * p.v_s1;
-    const unsigned vsize = (unsigned)((int64_t)(a - 1) * p.v_s2 + 4 * D);
-    const rsrc_t r = make_rsrc(vbase, vsize);
-    const int pieces = a * D / 4, ppr = D / 4;
-    for (int i0 = kWave * wv; i0 < pieces; i0 += kExactThreads) {
-      const int i = i0 + lane;
-      const unsigned off = i < pieces ? (unsigned)((int64_t)(i / ppr) * p.v_s2 + 16 * (i % ppr)) : vsize;
+  const int pieces = a * PPR;
+  // rows of one KV head from base into LDS: piece i is physical slot i % PPR
+  // of row i / PPR, which holds logical slot (i % PPR) ^ sw(row); pieces past
+  // the row arrive as zeros. Waves w0.. w0 + nw - 1 share the requests.
+  auto rows_to_lds = [&](const char* base, int64_t s2, bool swizzle, int w0, int nw) __attribute__((always_inline)) {
+    const unsigned size = (unsigned)((int64_t)(a - 1) * s2 + 4 * D);
+    const rsrc_t r = make_rsrc(base, size);
+    for (int i0 = kWave * (wv - w0); i0 < pieces; i0 += kWave * nw) {
+      const int i = i0 + lane, row = i / PPR, slot = i % PPR;
+      const int ls = swizzle ? slot ^ swz<PPR>(row) : slot;
+      const unsigned off = i < pieces ? (unsigned)((int64_t)row * s2 + 16 * ls) : size;
       dma16(r, (lds_t*)ex_lds + 16 * i0, off);
     }
-  }
-  // one key's score per thread, d ascending, product and sum each rounded
+  };
+  rows_to_lds(p.k + kvh * p.k_s1, p.k_s2, true, 0, kExactThreads / kWave);
+  // this wave's query elements into registers meanwhile
   const float* q = reinterpret_cast<const float*>(p.q + h * p.q_s1 + (int64_t)j * p.q_s2);
+  float4 qv[PPR];
+#pragma unroll
+  for (int u = 0; u < PPR; ++u) qv[u] = *reinterpret_cast<const float4*>(q + 4 * u);
+  wait_vmem<0>();  // this wave's K requests (and the query) have landed
+  wg_barrier();
+  // one key's score per thread, d ascending, product and sum each rounded
   float mx = -INFINITY;
   for (int i = tid; i < a; i += kExactThreads) {
-    const float* kr = reinterpret_cast<const float*>(p.k + kvh * p.k_s1 + (int64_t)i * p.k_s2);
-    float4 kv[D / 4];
+    const lds_t* const rowp = (const lds_t*)ex_lds + i * (4 * D);
+    // the D products first (independent), then their sum in order
+    float pr[D];
 #pragma unroll
-    for (int u = 0; u < D / 4; ++u) kv[u] = *reinterpret_cast<const float4*>(kr + 4 * u);
+    for (int u = 0; u < PPR; ++u) {
+      const f32x4_t kv = lds_load<f32x4_t>(rowp + 16 * (u ^ swz<PPR>(i)));
+      pr[4 * u] = kv.x * qv[u].x;
+      pr[4 * u + 1] = kv.y * qv[u].y;
+      pr[4 * u + 2] = kv.z * qv[u].z;
+      pr[4 * u + 3] = kv.w * qv[u].w;
+    }
     float acc = 0.0f;
 #pragma unroll
-    for (int u = 0; u < D / 4; ++u) {
-      const float4 qv = *reinterpret_cast<const float4*>(q + 4 * u);
-      acc = acc + kv[u].x * qv.x;
-      acc = acc + kv[u].y * qv.y;
-      acc = acc + kv[u].z * qv.z;
-      acc = acc + kv[u].w * qv.w;
-    }
+    for (int d = 0; d < D; ++d) acc = acc + pr[d];
     const float v = acc * p.scale;
     prob[i] = v;
     mx = v > mx ? v : mx;
@@ -242,20 +291,24 @@ __global__ __launch_bounds__(kExactThreads) void attn_exact_staged_kernel(const 
   }
   if (tid < 32) tab[tid] = te;
   if (lane == 0) red[wv] = mx;
-  __syncthreads();
-  mx = red[0];
-  for (int w = 1; w < kExactThreads / kWave; ++w) mx = red[w] > mx ? red[w] : mx;
-  for (int i = tid; i < a; i += kExactThreads) prob[i] = expf_ref(prob[i] - mx, tab);
-  __syncthreads();
-  if (tid == 0) {
-    const float sum = exact_sum(prob, a);
-    red[4] = (float)(1.0 / (double)sum);  // the correctly rounded 1.0f / sum
+  wg_barrier();  // the scores are in LDS and every K row has been read
+  if (wv > 0) {
+    rows_to_lds(p.v + kvh * p.v_s1, p.v_s2, false, 1, kExactThreads / kWave - 1);
+    wait_vmem<0>();  // this wave's V requests have landed
+  } else {
+    mx = red[0];
+    for (int w = 1; w < kExactThreads / kWave; ++w) mx = red[w] > mx ? red[w] : mx;
+    for (int i = lane; i < a; i += kWave) prob[i] = expf_ref(prob[i] - mx, tab);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the wave's exponentials are in LDS
+    if (lane == 0) {
+      const float sum = exact_sum(prob, a);
+      red[4] = (float)(1.0 / (double)sum);  // the correctly rounded 1.0f / sum
+    }
   }
-  __syncthreads();
+  wg_barrier();  // the V rows and 1 / sum
   const float inv = red[4];
   for (int i = tid; i < a; i += kExactThreads) prob[i] = prob[i] * inv;
-  wait_vmem<0>();  // this wave's V requests have landed
-  __syncthreads();
+  wg_barrier();
   if (tid < D) {
     const float acc = exact_dot<D>(vl + tid, prob, a);
     float* out = reinterpret_cast<float*>(p.out + h * p.o_s1 + (int64_t)j * p.o_s2);
