@@ -10,11 +10,12 @@
 //   O[o] = sum_t V[o, kvh, t] * P_t            t ascending (masked t add +-0, skipped)
 //
 // Rows whose keys' V fit in LDS (a * head_dim * 4 <= kExactStageBytes) run
-// attn_exact_staged_kernel: 256 threads per (token j, head h); the row's V
-// rows are requested into LDS (LDS-direct, 16 bytes per lane) at the start and
-// land while the threads form one key's score each, the maximum, and the
-// exponentials; lane 0 runs the ordered sum; then each output element's lane
-// runs its ordered V sum from LDS. Longer rows run attn_exact_kernel: one wave
+// attn_exact_staged_kernel: 256 threads per (token j, head h); the row's K
+// rows come into LDS (LDS-direct, coalesced) and the threads form one key's
+// score each from there; then three waves bring the V rows over the K rows
+// while wave 0 forms the maximum, the exponentials and (lane 0) the ordered
+// sum; then each output element's lane runs its ordered V sum from LDS.
+// Longer rows run attn_exact_kernel: one wave
 // per (token, head), lanes splitting the keys and then the output elements,
 // V read from global memory. Either way the ordered sums make a row's cost
 // linear in its key count on one lane: this is the checking path for
