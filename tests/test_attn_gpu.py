@@ -126,6 +126,23 @@ def test_decode_f16_cache_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv, decod
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
 
 
+# The library's own choice for an F16 cache (MI_HIP_DECODE_AUTO, no fixture):
+# heads split on the vector units where the split launch's waves stream fewer
+# than 4 sub-tiles (one layer of the 0.5B shape at n_kv 512-8192, the 7B shape
+# at 512), whole on the matrix cores otherwise (32768; the 7B shape at 4096
+# and 8192).
+@pytest.mark.parametrize("n_rep,hkv,d,n_kv", [(7, 2, 64, 512), (7, 2, 64, 1024), (7, 2, 64, 4096),
+                                              (7, 2, 64, 8192), (7, 2, 64, 32768), (7, 4, 128, 512),
+                                              (7, 4, 128, 4096), (7, 4, 128, 8192)])
+def test_decode_f16_cache_default_choice(hip, stream, oracle, n_rep, hkv, d, n_kv):
+    print("f16 decode, default kernel choice", n_rep, hkv, d, n_kv, flush=True)
+    q, k, v = cpu_attention.make_inputs(1900 + n_kv + d, d, n_rep * hkv, hkv, n_kv, 1)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_kv - 1, scale, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale, f16=True), TOL_F32, "widened")
+    assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, scale), TOL_F16, "unrounded")
+
+
 @pytest.fixture(params=[mh.MI_HIP_DECODE_MATRIX, mh.MI_HIP_DECODE_VALU, mh.MI_HIP_DECODE_STREAM],
                 ids=["matrix", "valu", "stream"])
 def decode_mode(request, hip):
