@@ -478,7 +478,6 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     reset(blk(u));
     wait_vmem<0>();
     read_k(kk);
-    sc = qk(kk);
     int un = take();
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the tile is read before it is refilled
     if (un < T) request_k(unit_tile(un));
@@ -486,6 +485,7 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     // (after the K request: every K request is followed by exactly NVL loads
     // before the wait that reads its tile)
     load_v(unit_tile(u), vv);
+    sc = qk(kk);
     while (un < T) {
       // sc: scores of unit u; the LDS tile is filling with unit un's K
       const int unn = take();
@@ -498,6 +498,10 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       wait_vmem<C::WAIT_K>();
       read_k(kk);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the whole A operand at once
+      // The tile is read: refill it with unit unn's K now, so that the load
+      // has this iteration's products to land behind (no request past the
+      // wave's last unit: its region becomes a record).
+      if (unn < T) request_k(unit_tile(unn));
       __builtin_amdgcn_sched_barrier(0);
       const floatx16 sn = qk(kk);
       softmax(sc);
@@ -511,9 +515,6 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
           __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
         }
       }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      // no request past the wave's last unit (its region becomes a record)
-      if (unn < T) request_k(unit_tile(unn));
       __builtin_amdgcn_sched_barrier(0);
       rescale_o();
       pv(sc, vv);
