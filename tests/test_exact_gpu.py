@@ -7,7 +7,9 @@ rows in LDS, the ordered sums read in chunks of 16 ahead of their additions);
 longer rows run the unstaged kernel. Key counts cover one key, partial and
 whole chunks of 16, odd and even chunk counts, the staged limit and past it,
 prefill rows on both sides of it, and a row whose exponentials are all equal
-but one (its one-lane sum rounds the same way step after step).
+but one (its one-lane sum rounds the same way step after step). 32 seeded
+random shapes (1-8 KV heads, 1-8 Q heads each, decode rows and short
+prefills, 1-3000 keys) cover head layouts the chosen cases do not.
 """
 import ctypes
 
@@ -91,3 +93,28 @@ def test_rejects_what_it_does_not_cover(hip, stream):
     a = mh.attn_args(q, out, 7, 39999, 0.125, stream, k=k, v=k)
     assert hip.mi_hip_attn_fwd_reference_order(ctypes.byref(a)) == 5
     assert "32768" in hip.last_error()
+
+
+def _random_cases(n, seed):
+    # (case, n_head_kv, n_rep, head_dim, n_past, n_tokens, scale): decode rows and
+    # short prefills, key counts spread log-uniformly over 1..3000 (the staged
+    # kernel below 512 keys at head_dim 64 / 256 at 128, the unstaged above)
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.choice([1, 2, 3, 4, 8]))
+        n_rep = int(rng.integers(1, 9))
+        d = int(rng.choice([64, 128]))
+        n_kv = max(1, int(np.exp(rng.uniform(0.0, np.log(3000.0)))))
+        n_tok = 1 if rng.uniform() < 0.6 else int(rng.integers(2, min(n_kv, 40) + 1)) if n_kv > 1 else 1
+        scale = float(np.float32(rng.uniform(0.5, 2.0) / np.sqrt(d)))
+        out.append((i, hkv, n_rep, d, n_kv - n_tok, n_tok, scale))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_cases(32, 20261204), ids=lambda c: f"r{c[0]}")
+def test_random_shapes_bit_for_bit(hip, stream, case):
+    i, hkv, n_rep, d, n_past, n_tok, scale = case
+    q, k, v = _inputs(3000 + i, n_tok, n_past + n_tok, hkv * n_rep, hkv, d)
+    _check(hip, stream, q, k, v, n_past, scale,
+           f"random case {i}: n_head_kv {hkv} n_rep {n_rep} D {d} n_past {n_past} n_tokens {n_tok}")
