@@ -3,7 +3,9 @@
 - mi_hip_op_attn_qk / mi_hip_op_attn_kqv accumulate in the reference's order
   with separately rounded multiply and add, and mi_hip_op_softmax sums in key
   order with the glibc expf restated, so on the reference's own inputs they
-  must reproduce the scores / probabilities / output BIT FOR BIT.
+  must reproduce the scores / probabilities / output BIT FOR BIT, on the
+  reference's goldens and on 24 seeded random shapes (head_dim 4..128, F32
+  and F16 caches, decode rows and short prefills) against the oracle.
 - The executor hook runs a host-resident graph shaped like the engine's
   (src/model_qwen2.cpp:153-177: K/V CPY into the cache, ATTN_QK, SOFTMAX,
   ATTN_KQV) with the threading contract of src/threadpool.cpp:171-180, and
@@ -207,3 +209,54 @@ def test_executor_hook_refuses_unplanned_device_kv(hip):
         assert "prepare" in hip.last_error()
     finally:
         hip.check(hip.mi_hip_kv_destroy(kv))
+
+
+def _random_node_cases(n, seed):
+    # (case, n_head_kv, n_rep, head_dim, n_past, n_tokens, f16, scale): the node
+    # kernels take any head_dim, so the shapes include ones the fused kernels
+    # do not (4..128)
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        hkv = int(rng.integers(1, 5))
+        n_rep = int(rng.integers(1, 9))
+        d = int(rng.choice([4, 8, 16, 32, 64, 80, 96, 128]))
+        n_kv = max(1, int(np.exp(rng.uniform(0.0, np.log(700.0)))))
+        n_tok = 1 if rng.uniform() < 0.5 or n_kv == 1 else int(rng.integers(2, min(n_kv, 20) + 1))
+        f16 = bool(rng.integers(0, 2))
+        scale = float(np.float32(1.0 / np.sqrt(d)))
+        out.append((i, hkv, n_rep, d, n_kv - n_tok, n_tok, f16, scale))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_node_cases(24, 20261205), ids=lambda c: f"n{c[0]}")
+def test_node_ops_random_shapes_bit_for_bit(hip, stream, case):
+    import torch
+    i, hkv, n_rep, d, n_past, n_tok, f16, scale = case
+    print(f"node case {i}: n_head_kv {hkv} n_rep {n_rep} D {d} n_past {n_past} n_tokens {n_tok} f16 {f16}",
+          flush=True)
+    n_head, n_kv = hkv * n_rep, n_past + n_tok
+    q, k, v = cpu_attention.make_inputs(4000 + i, d, n_head, hkv, n_kv, n_tok)
+    dq = dev(q)
+    dk = dev(k.astype(np.float16)) if f16 else dev(k)
+    dv = dev(v.astype(np.float16)) if f16 else dev(v)
+    kt = mh.MI_TYPE_F16 if f16 else mh.MI_TYPE_F32
+    elt = 2 if f16 else 4
+    tq, tk, tv = dtensor(dq), dtensor(dk, elt, kt), dtensor(dv, elt, kt)
+    scores = torch.full((n_head, n_tok, n_kv), float("nan"), device="cuda")
+    probs = torch.full_like(scores, float("nan"))
+    out = torch.full((n_tok, n_head, d), float("nan"), device="cuda")
+    ts = dtensor(scores, op=mh.MI_OP_ATTN_QK, src=[tq, tk], params=[n_past, n_rep])
+    tp = dtensor(probs, op=mh.MI_OP_SOFTMAX, src=[ts], params=[n_past, scale])
+    to = dtensor(out, op=mh.MI_OP_ATTN_KQV, src=[tp, tv], params=[n_rep])
+    hip.check(hip.mi_hip_op_attn_qk(ctypes.byref(ts), stream))
+    hip.check(hip.mi_hip_op_softmax(ctypes.byref(tp), stream))
+    hip.check(hip.mi_hip_op_attn_kqv(ctypes.byref(to), stream))
+    torch.cuda.synchronize()
+    if f16:
+        k = cpu_attention.fp16_widen(k.astype(np.float16))
+        v = cpu_attention.fp16_widen(v.astype(np.float16))
+    want_s, want_p, want_o = cpu_attention.oracle().attention(q, k, v, n_past, scale, 4)
+    assert np.array_equal(bits(scores.cpu().numpy()), bits(want_s)), f"node case {i}: scores differ"
+    assert np.array_equal(bits(probs.cpu().numpy()), bits(want_p)), f"node case {i}: probs differ"
+    assert np.array_equal(bits(out.cpu().numpy()), bits(want_o)), f"node case {i}: output differs"
