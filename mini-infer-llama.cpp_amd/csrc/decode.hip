@@ -1390,11 +1390,14 @@ int decode_team(int head_dim, bool f16, int group) {
   return threads / (hsl * head_dim / 4) * 8;
 }
 
+// A KV head's n_rep Q heads go in as few chunks of at most 8 as there can be
+// (each chunk's workgroups read the KV head's rows once), cut as evenly as
+// the kernels cut them: chunk hc holds heads [hc n_rep / c, (hc + 1) n_rep / c).
+int decode_chunks(int n_rep) { return (n_rep + 7) / 8; }
+
 int decode_group_size(int n_rep) {
-  static const int kSizes[] = {8, 7, 6, 5, 4, 3, 2, 1};
-  for (int g : kSizes)
-    if (n_rep % g == 0) return g;
-  return 1;
+  const int c = decode_chunks(n_rep);
+  return (n_rep + c - 1) / c;
 }
 
 size_t decode_record_floats(int head_dim, int group) {

@@ -11,7 +11,8 @@
 namespace mi {
 
 // decode.hip
-int decode_group_size(int n_rep);                       // G: Q heads per group
+int decode_chunks(int n_rep);                           // head chunks per KV head
+int decode_group_size(int n_rep);                       // G: Q heads of the widest chunk
 int decode_wg_waves(int head_dim, bool f16);            // waves per decode workgroup
 int decode_ring_slots(int head_dim, bool f16);          // ring slots per wave
 size_t decode_record_floats(int head_dim, int group);   // floats per cross-workgroup record

@@ -190,7 +190,7 @@ bool plan_stream(DecodePlan& p, mi::DecodeItem* it, int n_items, int n_head_kv, 
   if (head_dim != 64 && head_dim != 128) return false;
   p = DecodePlan{};
   p.group = mi::decode_group_size(n_rep);
-  p.n_chunks = n_rep / p.group;
+  p.n_chunks = mi::decode_chunks(n_rep);
   const int gpi = n_head_kv * p.n_chunks;
   int64_t sub = 0;
   for (int i = 0; i < n_items; ++i) {
@@ -263,7 +263,7 @@ DecodePlan plan_decode(mi::DecodeItem* it, int n_items, int n_head_kv, int n_rep
                        bool f16, int max_groups) {
   DecodePlan p;
   p.group = mi::decode_group_size(n_rep);
-  p.n_chunks = n_rep / p.group;
+  p.n_chunks = mi::decode_chunks(n_rep);
   const int waves = mi::decode_wg_waves(head_dim, f16);
   const int ring = waves * mi::decode_ring_slots(head_dim, f16);
   const int pos_bytes = 2 * head_dim * (f16 ? 2 : 4);
@@ -380,7 +380,7 @@ void ws_layout(mi_hip_workspace* ws, char* base, int groups, size_t rec_bytes) {
 void ws_capacity(int n_head_kv, int n_rep, int head_dim, int* groups, size_t* rec_bytes) {
   const int group = mi::decode_group_size(n_rep);
   // a head split doubles the groups (records stay: each holds half the heads)
-  const int64_t gr = (int64_t)mi::kDecodeMaxItems * n_head_kv * (n_rep / group) * (group > 4 ? 2 : 1);
+  const int64_t gr = (int64_t)mi::kDecodeMaxItems * n_head_kv * mi::decode_chunks(n_rep) * (group > 4 ? 2 : 1);
   const int64_t wgs = g.knobs.kpg > 0 ? gr * g.knobs.kpg : g.n_cu + gr;
   *groups = (int)gr;
   *rec_bytes = (size_t)wgs * mi::decode_record_floats(head_dim, group) * sizeof(float);

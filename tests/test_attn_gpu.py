@@ -78,10 +78,15 @@ def test_decode_sweep_qwen05_shape(hip, stream, oracle, n_kv, decode_mode):
     assert_close(got, ref_out(oracle, q, k, v, n_kv - 1, 0.125), TOL_F32, f"n_kv={n_kv}")
 
 
+# More than 8 Q heads per KV head go in ceil(n_rep / 8) chunks cut as evenly
+# as they can be, whatever n_rep's divisors (9 -> 4 + 5, 11 -> 5 + 6,
+# 13 -> 6 + 7, 15 -> 7 + 8, 17 -> 5 + 6 + 6), at short and long contexts.
 @pytest.mark.parametrize("n_rep,hkv,d", [(1, 4, 64), (2, 2, 64), (4, 2, 128), (8, 2, 64),
-                                         (3, 2, 64), (6, 1, 128), (14, 1, 64)])
-def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d, decode_mode):
-    n_kv = 777
+                                         (3, 2, 64), (6, 1, 128), (14, 1, 64), (9, 2, 64),
+                                         (11, 2, 64), (13, 1, 128), (15, 2, 64), (16, 2, 128),
+                                         (17, 1, 64), (24, 1, 64)])
+@pytest.mark.parametrize("n_kv", [777, 5000])
+def test_decode_group_shapes(hip, stream, oracle, n_rep, hkv, d, n_kv, decode_mode):
     q, k, v = cpu_attention.make_inputs(31 + n_rep, d, n_rep * hkv, hkv, n_kv, 1)
     scale = float(np.float32(1) / np.sqrt(np.float32(d)))
     got = fused(hip, stream, q, k, v, n_kv - 1, scale)
