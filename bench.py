@@ -453,8 +453,8 @@ def cpu_reference_engine(path, prompt_path, threads=16):
 
 
 def cpu_share():
-    """Host cores this process may use on the box: its affinity set, capped at
-    the 16 cores a one-GPU box grants a job (its OMP_NUM_THREADS)."""
+    """Host cores this process may use: its affinity set, capped at
+    OMP_NUM_THREADS and at 16 (one GPU's share of an 8-GPU MI355X host)."""
     try:
         allowed = len(os.sched_getaffinity(0))
     except OSError:

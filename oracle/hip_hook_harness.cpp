@@ -3,8 +3,8 @@
 //
 // Linked into the reference CLI (src/main.cpp and the core sources, compiled
 // where they lie) with GNU ld's --wrap, so that the reference's unmodified
-// call sites reach the product library through the integration points that
-// INTEGRATION.md documents:
+// call sites reach the product library through the four integration points
+// a maintainer adds to the engine:
 //   mi_compute_forward      (src/ops_cpu.cpp:481; called by every pool thread,
 //                            src/threadpool.cpp:171-180, by the pool-less
 //                            src/graph.cpp:75-83, and by the dump path,

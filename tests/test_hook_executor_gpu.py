@@ -5,7 +5,8 @@ sources, compiled where they lie) with oracle/hip_hook_harness.cpp linked in
 and GNU ld --wrap on mi_compute_forward, mi_gallocr_alloc_graph and
 mi_kv_cache_init/_free: the reference's unmodified thread pool, graph
 allocator and dump path call mi_hip_compute_forward / mi_hip_graph_prepare /
-mi_hip_kv_create + mi_hip_kv_bind exactly where INTEGRATION.md places them.
+mi_hip_kv_create + mi_hip_kv_bind at the four points a maintainer adds to
+the engine (mi_compute_forward, mi_graph_compute, mi_kv_cache_init/_free).
 oracle/_ref/mini_infer is the same CLI without the hooks.
 
 Paths exercised: the pool (every thread calls mi_compute_forward for every
