@@ -355,7 +355,7 @@ void decode_kernel(const DecodeParams p) {
   // Rows are as wide as the launch's widest item.
   if ((int)blockIdx.x >= a_gpi * kpg) return;
   const int wg = wg0 + (int)blockIdx.x;  // this workgroup's record
-  if (!DYN) {
+  if (!DYN && !a_det) {  // (deterministic takes use no counter: no barrier to start)
     if (threadIdx.x == 0) lds_store<unsigned>(lds + C::L_FLAG + 4, 0u);  // LDS take counter
     wg_barrier();
   }
