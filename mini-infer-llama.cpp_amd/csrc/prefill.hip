@@ -239,11 +239,11 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   // db's row c is therefore dim NDB c + db (write_record puts dims back in
   // order).
   const unsigned vvo = (unsigned)(4 * kh * vs2 + col * NDB * ELT);
-  auto load_v = [&](int kt, float (&vv)[NV]) __attribute__((always_inline)) {
+  // key t's V values of key tile kt into vv[NDB t ..]
+  auto load_v_key = [&](int kt, int t, float (&vv)[NV]) __attribute__((always_inline)) {
     const int key0 = kt * kPrefillKeys;
     const unsigned to_lane = key0 + kPrefillKeys <= n_kv ? 0u : ~0u;
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
+    {
       const unsigned row = (unsigned)((key0 + 8 * (t >> 2) + (t & 3)) * vs2);
       const unsigned vo = vvo + (row & to_lane), so = row & ~to_lane;
       if constexpr (ELT == 4 && NDB == 2) {
@@ -264,6 +264,10 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
         for (int db = 0; db < 4; ++db) vv[4 * t + db] = (float)x[db];
       }
     }
+  };
+  auto load_v = [&](int kt, float (&vv)[NV]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) load_v_key(kt, t, vv);
   };
 
   // The first unit of each wave is fixed (unit `wave`): its K tile is
@@ -465,6 +469,25 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
           o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t * NDB + db], s[t], o[db], 0, 0, 0);
     }
   };
+  // Float products with an F32 cache: the PV products of one tile, each key's
+  // V registers reloaded with key tile kt's values as soon as its products
+  // have read them, so that the next unit's V has the rest of this PV and the
+  // next QK to land behind (one buffer, the same 16 requests in key order).
+  constexpr bool PV_INTERLEAVE = !SPLIT && ELT == 4;
+  auto pv_load_v = [&](const floatx16& s, float (&vv)[NV], int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[t * NDB + db], s[t], o[db], 0, 0, 0);
+      load_v_key(kt, t, vv);
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NDB, 0);  // the key's MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // then its V load
+    }
+  };
 
   // The wave's units, software-pipelined (see the header). Request order per
   // iteration: the next unit's K tile, then the current V loads; the wait
@@ -517,12 +540,16 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
       }
       __builtin_amdgcn_sched_barrier(0);
       rescale_o();
-      pv(sc, vv);
+      if constexpr (PV_INTERLEAVE) {
+        pv_load_v(sc, vv, unit_tile(un));
+      } else {
+        pv(sc, vv);
+      }
       if (Xn != Xu) {
         write_record(0);  // this wave's part of block qa
         reset(Xn);
       }
-      load_v(unit_tile(un), vv);
+      if constexpr (!PV_INTERLEAVE) load_v(unit_tile(un), vv);
       sc = sn;
       u = un;
       un = unn;
