@@ -301,14 +301,26 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   }
   __syncthreads();
   // The next unit: from the LDS counter, or (deterministic launches) the
-  // wave's fixed sequence wave + NW, wave + 2 NW, ..., so that which wave
-  // computes which unit, and with it every rounding, is the same on every run.
-  int seq = wave;
+  // wave's fixed sequence, so that which wave computes which unit, and with
+  // it every rounding, is the same on every run: rounds of NW units, wave w
+  // taking unit w of each, except that with two waves per SIMD (NW = 8) the
+  // last round's units (when there is more than one round) go to the first
+  // NW/2 waves, two each. The two waves of a SIMD share its matrix core and
+  // the issue arbiter favours the older (the first NW/2): with equal shares
+  // the younger finished its last units alone, 4 us after the older (n=1024;
+  // moving them took 81.4 to 82.6 TFLOP/s). A unit index >= T means none.
+  int seq = 0;  // index in the wave's sequence of the unit last taken
   const int det = __builtin_amdgcn_readfirstlane(p.det);
+  constexpr int kShiftRounds = 1;  // (2 measured slower at n=1024, 80.2 against 82.7 TFLOP/s)
+  const int last_round = (T - 1) / NW;
+  const int shift0 = max(last_round - kShiftRounds + 1, 1);  // first shifted round
   auto take = [&]() __attribute__((always_inline)) {
     if (det) {
-      seq += NW;
-      return seq;
+      ++seq;
+      if (NW <= 4 || T <= NW || seq < shift0) return seq * NW + wave;
+      if (wave >= NW / 2) return T;
+      const int i = seq - shift0;  // the wave's i-th unit of the shifted rounds
+      return i < 2 * (last_round - shift0 + 1) ? shift0 * NW + i * (NW / 2) + wave : T;
     }
     unsigned t = 0;
     if (lane == 0) t = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
