@@ -118,3 +118,65 @@ def test_prefill_linear_in_values(hip, stream, prefill_products):
     o2 = fused(hip, stream, q, k, v2, 0, SCALE)
     o12 = fused(hip, stream, q, k, v1 + v2, 0, SCALE)
     assert_close(o12, (o1.astype(np.float64) + o2), TOL_F32, "O(V1 + V2) vs O(V1) + O(V2)")
+
+
+# The longest contexts one KV head's 32-bit byte offsets address: F32,
+# head_dim 64, 2 KV heads interleaved (512 bytes per position). Decode:
+# n_kv = 2^22 (the last row ends 256 bytes below 2^31). Prefill: 2^22 - 33
+# (its key tiles reach 32 rows past n_kv). Every key is zero except one per KV
+# head, aligned with every query so that its score is 40: weight e^40 against
+# fewer than 2^22 < e^15.3 for all the rest, so every head's output is that
+# position's V row (relative error below e^-24). Decode puts them at the very
+# last position (KV head 0) and in the middle (KV head 1); prefill at the last
+# cached position and in the middle, which all its queries see. One position
+# more is refused before anything runs (the buffers hold 64 rows more, so no
+# access could leave them either way).
+N_DECODE_MAX = 1 << 22
+N_PREFILL_MAX = (1 << 22) - 33
+
+
+def _dominant_keys(torch, n_rows, stars, seed):
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    k = torch.zeros((n_rows, HKV, D), device="cuda")
+    v = torch.randn((n_rows, HKV, D), device="cuda", generator=gen)
+    for g, pos in enumerate(stars):
+        k[pos, g] = 40.0 / (SCALE * D)
+    want = np.stack([v[stars[h // (H // HKV)], h // (H // HKV)].cpu().numpy() for h in range(H)])
+    return k, v, want
+
+
+def test_decode_longest_context(hip, stream, kernel):
+    import ctypes
+    import torch
+    print("longest decode context", kernel, N_DECODE_MAX, flush=True)
+    stars = (N_DECODE_MAX - 1, N_DECODE_MAX // 2 + 3)
+    k, v, want = _dominant_keys(torch, N_DECODE_MAX + 64, stars, 77)
+    q = torch.ones((1, H, D), device="cuda")
+    out = torch.full_like(q, float("nan"))
+    a = mh.attn_args(q, out, H // HKV, N_DECODE_MAX - 1, SCALE, stream, k=k, v=v)
+    hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), want[None], TOL_F32, "dominant keys at n_kv 2^22")
+    a = mh.attn_args(q, out, H // HKV, N_DECODE_MAX, SCALE, stream, k=k, v=v)
+    assert hip.mi_hip_attn_fwd(ctypes.byref(a)) == 5  # MI_HIP_E_UNSUPPORTED
+    assert "2^31" in hip.last_error()
+
+
+def test_prefill_longest_context(hip, stream, prefill_products):
+    import ctypes
+    import torch
+    n_tok = 32
+    n_past = N_PREFILL_MAX - n_tok
+    print("longest prefill context", prefill_products, N_PREFILL_MAX, flush=True)
+    stars = (n_past - 1, n_past // 2 + 5)
+    k, v, want = _dominant_keys(torch, N_PREFILL_MAX + 64, stars, 78)
+    q = torch.ones((n_tok, H, D), device="cuda")
+    out = torch.full_like(q, float("nan"))
+    a = mh.attn_args(q, out, H // HKV, n_past, SCALE, stream, k=k, v=v)
+    hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), np.broadcast_to(want[None], (n_tok, H, D)), TOL_F32,
+                 f"dominant keys at n_kv {N_PREFILL_MAX}")
+    a = mh.attn_args(q, out, H // HKV, n_past + 1, SCALE, stream, k=k, v=v)
+    assert hip.mi_hip_attn_fwd(ctypes.byref(a)) == 5  # MI_HIP_E_UNSUPPORTED
+    assert "2^31" in hip.last_error()
