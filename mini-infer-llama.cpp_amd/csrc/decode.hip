@@ -1117,18 +1117,26 @@ void decode_kernel(const DecodeParams p) {
     const int t = lane / (D / 4), cq = lane % (D / 4);
     const int hs = wv + NWV * t;
     if (t < SPW && hs < HSL) {
+      // every wave's (m, l) and float4 first (one round of LDS reads), then
+      // the stable combine in wave order
+      f32x2 mlw[NWV];
+      f32x4 aw[NWV];
+#pragma unroll
+      for (int w = 0; w < NWV; ++w) {
+        const float* dw = dep_at(w);
+        mlw[w] = *reinterpret_cast<const f32x2*>(dw + HSL * D + 2 * hs);
+        aw[w] = *reinterpret_cast<const f32x4*>(dw + hs * D + 4 * cq);
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, dep_at(w)[HSL * D + 2 * hs]);
+      for (int w = 0; w < NWV; ++w) mx = fmaxf(mx, mlw[w].x);
       float lt = 0.f;
       f32x4 at = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < NWV; ++w) {
-        const float* dw = dep_at(w);
-        const float mw = dw[HSL * D + 2 * hs];
-        const float wt = mw == -INFINITY ? 0.f : fast_exp2(mw - mx);  // a wave with no sub-tile
-        lt += wt * dw[HSL * D + 2 * hs + 1];
-        at += wt * *reinterpret_cast<const f32x4*>(dw + hs * D + 4 * cq);
+        const float wt = mlw[w].x == -INFINITY ? 0.f : fast_exp2(mlw[w].x - mx);  // a wave with no sub-tile
+        lt += wt * mlw[w].y;
+        at += wt * aw[w];
       }
       if (kpg == 1) {
         if (hs < G) {
