@@ -120,10 +120,11 @@ def test_prefill_linear_in_values(hip, stream, prefill_products):
     assert_close(o12, (o1.astype(np.float64) + o2), TOL_F32, "O(V1 + V2) vs O(V1) + O(V2)")
 
 
-# The longest contexts one KV head's 32-bit byte offsets address: F32,
-# head_dim 64, 2 KV heads interleaved (512 bytes per position). Decode:
-# n_kv = 2^22 (the last row ends 256 bytes below 2^31). Prefill: 2^22 - 33
-# (its key tiles reach 32 rows past n_kv). Every key is zero except one per KV
+# The longest contexts one KV head's 32-bit byte offsets address: head_dim
+# 64, 2 KV heads interleaved (512 bytes per position with an F32 cache, 256
+# with F16). Decode: n_kv = 2^22 (F32) or 2^23 (F16), the last row ending
+# 256 (128) bytes below 2^31. Prefill: 33 positions fewer (its key tiles reach
+# 32 rows past n_kv). Every key is zero except one per KV
 # head, aligned with every query so that its score is 40: weight e^40 against
 # fewer than 2^22 < e^15.3 for all the rest, so every head's output is that
 # position's V row (relative error below e^-24). Decode puts them at the very
@@ -131,52 +132,62 @@ def test_prefill_linear_in_values(hip, stream, prefill_products):
 # cached position and in the middle, which all its queries see. One position
 # more is refused before anything runs (the buffers hold 64 rows more, so no
 # access could leave them either way).
-N_DECODE_MAX = 1 << 22
-N_PREFILL_MAX = (1 << 22) - 33
+N_DECODE_MAX = {"f32": 1 << 22, "f16": 1 << 23}
+N_PREFILL_MAX = {"f32": (1 << 22) - 33, "f16": (1 << 23) - 33}
 
 
-def _dominant_keys(torch, n_rows, stars, seed):
+def _dominant_keys(torch, n_rows, stars, seed, f16):
+    # (5.0 and the V rows are exact in the cache type; want is their float value)
     gen = torch.Generator(device="cuda").manual_seed(seed)
-    k = torch.zeros((n_rows, HKV, D), device="cuda")
-    v = torch.randn((n_rows, HKV, D), device="cuda", generator=gen)
+    dt = torch.float16 if f16 else torch.float32
+    k = torch.zeros((n_rows, HKV, D), device="cuda", dtype=dt)
+    v = torch.randn((n_rows, HKV, D), device="cuda", generator=gen).to(dt)
     for g, pos in enumerate(stars):
         k[pos, g] = 40.0 / (SCALE * D)
-    want = np.stack([v[stars[h // (H // HKV)], h // (H // HKV)].cpu().numpy() for h in range(H)])
+    want = np.stack([v[stars[h // (H // HKV)], h // (H // HKV)].float().cpu().numpy() for h in range(H)])
     return k, v, want
 
 
-def test_decode_longest_context(hip, stream, kernel):
+@pytest.mark.parametrize("cache", ["f32", "f16"])
+def test_decode_longest_context(hip, stream, kernel, cache):
     import ctypes
     import torch
-    print("longest decode context", kernel, N_DECODE_MAX, flush=True)
-    stars = (N_DECODE_MAX - 1, N_DECODE_MAX // 2 + 3)
-    k, v, want = _dominant_keys(torch, N_DECODE_MAX + 64, stars, 77)
+    n_max = N_DECODE_MAX[cache]
+    print("longest decode context", kernel, cache, n_max, flush=True)
+    stars = (n_max - 1, n_max // 2 + 3)
+    k, v, want = _dominant_keys(torch, n_max + 64, stars, 77, cache == "f16")
     q = torch.ones((1, H, D), device="cuda")
     out = torch.full_like(q, float("nan"))
-    a = mh.attn_args(q, out, H // HKV, N_DECODE_MAX - 1, SCALE, stream, k=k, v=v)
+    a = mh.attn_args(q, out, H // HKV, n_max - 1, SCALE, stream, k=k, v=v)
     hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
     torch.cuda.synchronize()
-    assert_close(out.cpu().numpy(), want[None], TOL_F32, "dominant keys at n_kv 2^22")
-    a = mh.attn_args(q, out, H // HKV, N_DECODE_MAX, SCALE, stream, k=k, v=v)
+    assert_close(out.cpu().numpy(), want[None], TOL_F32, f"dominant keys at n_kv {n_max}")
+    a = mh.attn_args(q, out, H // HKV, n_max, SCALE, stream, k=k, v=v)
     assert hip.mi_hip_attn_fwd(ctypes.byref(a)) == 5  # MI_HIP_E_UNSUPPORTED
     assert "2^31" in hip.last_error()
+    del k, v
+    torch.cuda.empty_cache()
 
 
-def test_prefill_longest_context(hip, stream, prefill_products):
+@pytest.mark.parametrize("cache", ["f32", "f16"])
+def test_prefill_longest_context(hip, stream, prefill_products, cache):
     import ctypes
     import torch
     n_tok = 32
-    n_past = N_PREFILL_MAX - n_tok
-    print("longest prefill context", prefill_products, N_PREFILL_MAX, flush=True)
+    n_max = N_PREFILL_MAX[cache]
+    n_past = n_max - n_tok
+    print("longest prefill context", prefill_products, cache, n_max, flush=True)
     stars = (n_past - 1, n_past // 2 + 5)
-    k, v, want = _dominant_keys(torch, N_PREFILL_MAX + 64, stars, 78)
+    k, v, want = _dominant_keys(torch, n_max + 64, stars, 78, cache == "f16")
     q = torch.ones((n_tok, H, D), device="cuda")
     out = torch.full_like(q, float("nan"))
     a = mh.attn_args(q, out, H // HKV, n_past, SCALE, stream, k=k, v=v)
     hip.check(hip.mi_hip_attn_fwd(ctypes.byref(a)))
     torch.cuda.synchronize()
     assert_close(out.cpu().numpy(), np.broadcast_to(want[None], (n_tok, H, D)), TOL_F32,
-                 f"dominant keys at n_kv {N_PREFILL_MAX}")
+                 f"dominant keys at n_kv {n_max}")
     a = mh.attn_args(q, out, H // HKV, n_past + 1, SCALE, stream, k=k, v=v)
     assert hip.mi_hip_attn_fwd(ctypes.byref(a)) == 5  # MI_HIP_E_UNSUPPORTED
     assert "2^31" in hip.last_error()
+    del k, v
+    torch.cuda.empty_cache()
