@@ -85,6 +85,8 @@ def test_status_and_errors_without_device(lib):
     a.n_rep = 7
     a.n_past, a.n_tokens = -1, 1
     assert lib.mi_hip_attn_fwd(ctypes.byref(a)) == 1
+    a.n_past, a.n_tokens = 5, 0  # no query: refused, not a silent no-op
+    assert lib.mi_hip_attn_fwd(ctypes.byref(a)) == 1 and "n_tokens" in lib.last_error()
     assert lib.mi_hip_attn_decode_batch(None, 0, None) == 1
     d = mh.KvDesc(0, 16, 2, 64, 14, 0)
     h = ctypes.c_void_p()
