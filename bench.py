@@ -222,11 +222,12 @@ def bench_decode_per_layer(torch, mh, lib, stream, steps, warmup, n_layers=24, n
     return dict(us_per_layer=ms * 1e3 / n_layers, gbps=nbytes / (ms * 1e-3) / 1e9)
 
 
-def bench_prefill(torch, mh, lib, stream, steps, warmup, n, h=14, hkv=2, d=64):
+def bench_prefill(torch, mh, lib, stream, steps, warmup, n, h=14, hkv=2, d=64, f16=False):
     gen = torch.Generator(device="cuda").manual_seed(n)
+    dt = torch.float16 if f16 else torch.float32
     q = torch.randn((n, h, d), device="cuda", generator=gen)
-    k = torch.randn((n, hkv, d), device="cuda", generator=gen)
-    v = torch.randn((n, hkv, d), device="cuda", generator=gen)
+    k = torch.randn((n, hkv, d), device="cuda", generator=gen).to(dt)
+    v = torch.randn((n, hkv, d), device="cuda", generator=gen).to(dt)
     o = torch.empty((n, h, d), device="cuda")
     a = mh.attn_args(q, o, h // hkv, 0, float(d) ** -0.5, stream, k=k, v=v)
 
@@ -620,9 +621,13 @@ def main():
         # the split-bf16 form beside the default float products
         lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_SPLIT_BF16))
         res["prefill1024_split"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024)
-        lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
+        lib.check(lib.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_AUTO))
+        # an F16 cache at the same shape (the default form for it: f16
+        # products, exact in the cache operand)
+        res["prefill1024_f16"] = bench_prefill(torch, mh, lib, stream, args.steps, args.warmup, 1024, f16=True)
         print(f"# prefill 1024: {res['prefill1024']['tflops']:.2f} TF/s, 4096: "
-              f"{res['prefill4096']['tflops']:.2f} TF/s", file=sys.stderr, flush=True)
+              f"{res['prefill4096']['tflops']:.2f} TF/s; F16 cache 1024: "
+              f"{res['prefill1024_f16']['tflops']:.2f} TF/s", file=sys.stderr, flush=True)
     if want("d7b"):
         res["decode7b"] = bench_decode(torch, mh, lib, stream, args.steps, args.warmup,
                                        n_layers=1, n_kv=8192, h=28, hkv=4, d=128, f16=True)
@@ -781,6 +786,17 @@ def main():
                 "issued_flops_per_launch": iss,
                 "issued_tflops_bf16": round(iss / ps["kernel_ms"] / 1e9, 2),
                 "frac_of_bf16_peak": round(iss / ps["kernel_ms"] / 1e9 / BF16_MFMA_PEAK_TFLOPS, 4)}
+        if "prefill1024_f16" in res:
+            pf = res["prefill1024_f16"]
+            # two f16 products per product step (Q and P as f16 pairs) over the
+            # same tiles as the float form: twice its issued FLOPs
+            iss = 2 * issued if issued else 2 * 1.03 * pf["flops"]
+            out["prefill"]["f16_cache_1024"] = {
+                "products": "f16 (v_mfma_f32_32x32x16_f16; the cache operand exact, Q and P as f16 pairs)",
+                "tflops_causal": round(pf["tflops"], 2), "us": round(pf["kernel_ms"] * 1e3, 2),
+                "issued_flops_per_launch": iss,
+                "issued_tflops_f16": round(iss / pf["kernel_ms"] / 1e9, 2),
+                "frac_of_f16_peak": round(iss / pf["kernel_ms"] / 1e9 / BF16_MFMA_PEAK_TFLOPS, 4)}
     if "sweep" in res:
         out["decode_sweep"] = {
             "workload": "24 independent layer caches, 1 query token, 14 Q / 2 KV heads, head_dim 64, "

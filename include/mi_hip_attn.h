@@ -145,19 +145,28 @@ int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim
 int mi_hip_set_deterministic(int32_t on);
 
 /* Matrix cores of the prefill kernel's QK and PV products.
- *   MI_HIP_PREFILL_F32 (the default): v_mfma_f32_32x32x2f32 (float
- *     products, as the reference's ops), within the 1e-4 bar at any score
- *     magnitude.
- *   MI_HIP_PREFILL_SPLIT_BF16: every float operand is split into a pair of
- *     bf16 (hi = round(x), lo = round(x - hi), |x - hi - lo| <= 2^-17 |x|)
- *     and each product is lo.hi + hi.lo + hi.hi on v_mfma_f32_32x32x16_bf16
- *     with float accumulation: ~2^-16 relative error per product, three bf16
- *     products at 16x the FP32 matrix rate. Within the 1e-4 bar only while
- *     scale * |q| * |k| stays small (N(0,1) inputs with q and k scaled by up
- *     to 2).
+ *   MI_HIP_PREFILL_AUTO (the default): MI_HIP_PREFILL_F32 with an F32 cache,
+ *     the split form below with an F16 cache (whose f16 products are exact
+ *     in the cache operand); within the 1e-4 bar at any score magnitude
+ *     either way.
+ *   MI_HIP_PREFILL_F32: v_mfma_f32_32x32x2f32 (float products, as the
+ *     reference's ops; an F16 cache widened to float), within the 1e-4 bar
+ *     at any score magnitude.
+ *   MI_HIP_PREFILL_SPLIT_BF16: with an F32 cache every float operand is split
+ *     into a pair of bf16 (hi = round(x), lo = round(x - hi),
+ *     |x - hi - lo| <= 2^-17 |x|) and each product is lo.hi + hi.lo + hi.hi
+ *     on v_mfma_f32_32x32x16_bf16 with float accumulation: ~2^-16 relative
+ *     error per product, three bf16 products at 16x the FP32 matrix rate,
+ *     within the 1e-4 bar only while scale * |q| * |k| stays small (N(0,1)
+ *     inputs with q and k scaled by up to 2). With an F16 cache the cache
+ *     operand is used as it is and Q and the probabilities are split into
+ *     f16 pairs (~2^-22 relative; a wave whose |q| exceeds 2^14 scales its
+ *     queries by a power of two first): two v_mfma_f32_32x32x16_f16 per
+ *     product step, within the bar at any score magnitude.
  * Process-wide. No counterpart in the reference. */
 #define MI_HIP_PREFILL_F32 0
 #define MI_HIP_PREFILL_SPLIT_BF16 1
+#define MI_HIP_PREFILL_AUTO 2
 int mi_hip_set_prefill_mode(int32_t mode);
 
 /* Products of the decode kernel (one query row per head).

@@ -43,6 +43,8 @@
 // is merged with the stable rescaling; nothing else leaves the workgroup. Two
 // waves per SIMD at head_dim 64 (one at 128) let one wave's vector work run
 // under the other's matrix-core work.
+#include <type_traits>
+
 #include "attn_common.h"
 #include "kernels.h"
 
@@ -113,6 +115,29 @@ __device__ inline void split8(const float* x, bf16x8& hi, bf16x8& lo) {
     hi[i] = h;
     lo[i] = (__bf16)(x[i] - (float)h);
   }
+}
+
+// F16 cache values (exact in f16) as f16, and float values x as an f16 pair
+// hi = RNE(x), lo = RNE(x - hi) (|x - hi - lo| <= 2^-22 |x| while lo is
+// normal, 2^-25 absolute below).
+__device__ inline void pack8h(const float* x, f16x8& v) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (_Float16)x[i];
+}
+__device__ inline void split8h(const float* x, f16x8& hi, f16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const _Float16 h = (_Float16)x[i];
+    hi[i] = h;
+    lo[i] = (_Float16)(x[i] - (float)h);
+  }
+}
+// acc += a . b over 16 k-values, a exact in f16 (the F16 cache operand), b
+// a float operand split into an f16 pair: a.b_lo + a.b_hi, two
+// v_mfma_f32_32x32x16_f16 (f16 products are exact in the float accumulator).
+__device__ inline floatx16 mfma2h(const f16x8& a, const f16x8& bh, const f16x8& bl, floatx16 acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bh, acc, 0, 0, 0);
 }
 
 // acc += a . b over 16 k-values with float inputs split into bf16 pairs:
@@ -383,12 +408,37 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
     }
   };
 
-  // The block's queries as bf16 pairs (SPLIT): step s, item i holds dim
-  // kh HALF + 8 s + i, the dims of kk[8 s + i] (any pairing of the k-values
-  // is a valid contraction as long as A and B agree).
-  bf16x8 qh[SPLIT ? HALF / 8 : 1], ql[SPLIT ? HALF / 8 : 1];
+  // The block's queries as bf16 pairs (SPLIT), or f16 pairs with an F16
+  // cache (F16P): step s, item i holds dim kh HALF + 8 s + i, the dims of
+  // kk[8 s + i] (any pairing of the k-values is a valid contraction as long
+  // as A and B agree). F16P: a wave whose largest |query| exceeds 2^14 takes
+  // its queries times 2^-e (exact), so that their f16 pairs stay in range,
+  // and its scores times 2^e.
+  constexpr bool F16P = SPLIT && ELT == 2;
+  typedef typename std::conditional<F16P, f16x8, bf16x8>::type qop_t;
+  qop_t qh[SPLIT ? HALF / 8 : 1], ql[SPLIT ? HALF / 8 : 1];
+  float qunscale = 1.f;
   auto split_q = [&]() __attribute__((always_inline)) {
-    if constexpr (SPLIT) {
+    if constexpr (F16P) {
+      float amax = 0.f;
+#pragma unroll
+      for (int i = 0; i < HALF; ++i) amax = fmaxf(amax, fabsf(qb[i]));
+      amax = wave_max(amax);
+      float f = 1.f;
+      qunscale = 1.f;
+      if (amax > 16384.f) {
+        const int e = ilogbf(amax) - 13;
+        f = ldexpf(1.f, -e);
+        qunscale = ldexpf(1.f, e);
+      }
+#pragma unroll
+      for (int st = 0; st < HALF / 8; ++st) {
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = qb[8 * st + i] * f;
+        split8h(x, qh[st], ql[st]);
+      }
+    } else if constexpr (SPLIT) {
 #pragma unroll
       for (int st = 0; st < HALF / 8; ++st) split8(qb + 8 * st, qh[st], ql[st]);
     }
@@ -398,7 +448,15 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   // v_mfma_f32_32x32x16_bf16 on bf16-pair-split operands
   auto qk = [&](const float (&kk)[HALF]) __attribute__((always_inline)) {
     floatx16 s = (floatx16)(0.f);
-    if constexpr (SPLIT) {
+    if constexpr (F16P) {
+#pragma unroll
+      for (int st = 0; st < HALF / 8; ++st) {
+        f16x8 k8;
+        pack8h(kk + 8 * st, k8);
+        s = mfma2h(k8, qh[st], ql[st], s);
+      }
+      if (qunscale != 1.f) s *= qunscale;
+    } else if constexpr (SPLIT) {
 #pragma unroll
       for (int st = 0; st < HALF / 8; ++st) {
         bf16x8 kh8, kl8;
@@ -455,7 +513,25 @@ __global__ __launch_bounds__(NW* kWave) void prefill_kernel(const PrefillParams 
   // 8u .. 8u + 7 of S^T (keys 8 (r / 4) + 4 kh + r % 4) and the V values of
   // the same keys
   auto pv = [&](const floatx16& s, const float (&vv)[NV]) __attribute__((always_inline)) {
-    if constexpr (SPLIT) {
+    if constexpr (F16P) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        float pf[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pf[i] = s[8 * u + i];
+        f16x8 ph, pl;
+        split8h(pf, ph, pl);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          float vf[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) vf[i] = vv[(8 * u + i) * NDB + db];
+          f16x8 v8;
+          pack8h(vf, v8);
+          o[db] = mfma2h(v8, ph, pl, o[db]);
+        }
+      }
+    } else if constexpr (SPLIT) {
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         float pf[8];

@@ -83,7 +83,7 @@ struct State {
   int n_cu = 0;  // compute units of the device
   Knobs knobs;
   std::atomic<int> deterministic{1};  // fixed per-wave takes in the fused kernels
-  std::atomic<int> prefill_mode{MI_HIP_PREFILL_F32};  // matrix cores of the prefill kernel
+  std::atomic<int> prefill_mode{MI_HIP_PREFILL_AUTO};  // matrix cores of the prefill kernel
   std::atomic<int> decode_mode{MI_HIP_DECODE_AUTO};          // matrix cores of the decode kernel
   mi_hip_workspace* default_ws = nullptr;  // for calls that name no workspace
   mi_hip_workspace* scratch_ws = nullptr;  // this device's entry of scratch_by_device
@@ -670,6 +670,13 @@ int run_decode(const mi_hip_attn_args* items, int n, hipStream_t stream, mi_hip_
   return MI_HIP_OK;
 }
 
+// Whether a prefill runs the split product form: asked for, or (AUTO) with an
+// F16 cache, whose f16 products are exact in the cache operand.
+bool prefill_split(bool f16) {
+  const int mode = g.prefill_mode.load();
+  return mode == MI_HIP_PREFILL_SPLIT_BF16 || (mode == MI_HIP_PREFILL_AUTO && f16);
+}
+
 int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream) {
   // a KV head's rows, up to the last key tile's end, are addressed with 32-bit
   // byte offsets
@@ -701,7 +708,7 @@ int run_prefill(const mi_hip_attn_args* a, const Resolved& r, hipStream_t stream
   p.scale_log2e = a->scale * kLog2e;
   p.det = g.deterministic.load();
   hipError_t e = mi::launch_prefill(p, r.head_dim, r.f16, g.n_cu,
-                                    g.prefill_mode.load() == MI_HIP_PREFILL_SPLIT_BF16, stream);
+                                    prefill_split(r.f16), stream);
   if (e != hipSuccess) return hip_fail(e, "prefill launch");
   return MI_HIP_OK;
 }
@@ -1116,8 +1123,10 @@ int mi_hip_decode_tuning(int32_t kpg, int32_t early, int32_t solo, int32_t claim
 }
 
 int mi_hip_set_prefill_mode(int32_t mode) {
-  if (mode != MI_HIP_PREFILL_F32 && mode != MI_HIP_PREFILL_SPLIT_BF16)
-    return fail(MI_HIP_E_INVALID, "prefill mode %d: MI_HIP_PREFILL_F32 (0) or MI_HIP_PREFILL_SPLIT_BF16 (1)", mode);
+  if (mode != MI_HIP_PREFILL_F32 && mode != MI_HIP_PREFILL_SPLIT_BF16 && mode != MI_HIP_PREFILL_AUTO)
+    return fail(MI_HIP_E_INVALID,
+                "prefill mode %d: MI_HIP_PREFILL_F32 (0), MI_HIP_PREFILL_SPLIT_BF16 (1) or MI_HIP_PREFILL_AUTO (2)",
+                mode);
   g.prefill_mode.store(mode);
   return MI_HIP_OK;
 }

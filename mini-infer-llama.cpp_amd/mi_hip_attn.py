@@ -30,6 +30,7 @@ MI_TENSOR_FLAG_KV = 1 << 3
 
 MI_HIP_PREFILL_F32 = 0
 MI_HIP_PREFILL_SPLIT_BF16 = 1
+MI_HIP_PREFILL_AUTO = 2
 MI_HIP_DECODE_VALU = 0
 MI_HIP_DECODE_MATRIX = 1
 MI_HIP_DECODE_AUTO = 2

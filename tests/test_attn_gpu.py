@@ -588,6 +588,55 @@ def test_prefill_f16_cache(hip, stream, oracle):
     assert_close(got, ref_out(oracle, q, k, v, 43, 0.125, f16=True), TOL_F32)
 
 
+# An F16 cache in every product mode: float products on the FP32 matrix
+# cores, or (the split mode, and the default for an F16 cache) f16 products,
+# exact in the cache operand, with Q and P as f16 pairs (~2^-22 per product),
+# at any score magnitude; queries beyond 2^14 in magnitude are scaled by a
+# power of two that the scores undo.
+@pytest.mark.parametrize("n_past,n_tok,d,h,hkv", [
+    (0, 1024, 64, 14, 2), (37, 100, 64, 14, 2), (0, 500, 128, 28, 4), (5, 200, 128, 8, 2), (300, 2, 64, 14, 2),
+])
+@pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_AUTO, mh.MI_HIP_PREFILL_SPLIT_BF16, mh.MI_HIP_PREFILL_F32])
+def test_prefill_f16_cache_vs_oracle(hip, stream, oracle, prefill_mode, mode, n_past, n_tok, d, h, hkv):
+    print("prefill f16", n_past, n_tok, d, h, hkv, mode, flush=True)
+    prefill_mode(mode)
+    q, k, v = cpu_attention.make_inputs(5777 + n_tok + d, d, h, hkv, n_past + n_tok + 3, n_tok)
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_past, scale, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, n_past, scale, f16=True), TOL_F32)
+
+
+@pytest.mark.parametrize("s", [2.0, 4.0])
+@pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_SPLIT_BF16, mh.MI_HIP_PREFILL_F32])
+def test_prefill_f16_cache_large_scores(hip, stream, oracle, prefill_mode, mode, s):
+    # q and k scaled by s (score standard deviation ~s^2 over N(0,1) inputs)
+    print("prefill f16 large scores", s, mode, flush=True)
+    prefill_mode(mode)
+    q, k, v = cpu_attention.make_inputs(6400 + int(s), 64, 14, 2, 300, 300)
+    q, k = (q * np.float32(s)).astype(np.float32), (k * np.float32(s)).astype(np.float32)
+    got = fused(hip, stream, q, k, v, 0, 0.125, f16=True)
+    assert_close(got, ref_out(oracle, q, k, v, 0, 0.125, f16=True), TOL_F32, f"s={s}")
+
+
+@pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_SPLIT_BF16, mh.MI_HIP_PREFILL_F32])
+def test_prefill_f16_cache_large_queries(hip, stream, oracle, prefill_mode, mode):
+    # Queries far outside the f16 range on some heads (|q| up to ~4e5), the
+    # others unscaled: the split mode's f16 query pairs are scaled by a power
+    # of two that the scores undo, and the result must not change.
+    print("prefill f16 large queries", mode, flush=True)
+    prefill_mode(mode)
+    n_past, n_tok, d = 40, 200, 128
+    q, k, v = cpu_attention.make_inputs(4343, d, 8, 2, n_past + n_tok, n_tok)
+    q = q.copy()
+    q[:, 1] *= 1e5
+    q[:, 6] *= 3e4
+    q[:, 7] *= 50.0
+    scale = float(np.float32(1) / np.sqrt(np.float32(d)))
+    got = fused(hip, stream, q, k, v, n_past, scale, f16=True)
+    assert np.isfinite(got).all()
+    assert_close(got, ref_out(oracle, q, k, v, n_past, scale, f16=True), TOL_F32, "widened")
+
+
 def test_prefill_4096_rows_equal_decode_oracle(hip, stream, oracle):
     # Size-independent property at the full n=4096: causal row j of a prefill
     # is exactly a decode at n_past = j, which the oracle runs in O(n).
@@ -645,7 +694,7 @@ def prefill_mode(hip):
     def set_(mode):
         hip.check(hip.mi_hip_set_prefill_mode(mode))
     yield set_
-    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
+    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_AUTO))
 
 
 @pytest.mark.parametrize("mode", [mh.MI_HIP_PREFILL_F32, mh.MI_HIP_PREFILL_SPLIT_BF16])

@@ -91,7 +91,7 @@ def test_decode_position_permutation(hip, stream, kernel, n_kv):
 def prefill_products(request, hip):
     hip.check(hip.mi_hip_set_prefill_mode(request.param))
     yield request.param
-    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_F32))
+    hip.check(hip.mi_hip_set_prefill_mode(mh.MI_HIP_PREFILL_AUTO))
 
 
 @pytest.mark.parametrize("n,m", [(1024, 1000), (4096, 2049)])
