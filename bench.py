@@ -789,8 +789,10 @@ def main():
         if "prefill1024_f16" in res:
             pf = res["prefill1024_f16"]
             # two f16 products per product step (Q and P as f16 pairs) over the
-            # same tiles as the float form: twice its issued FLOPs
-            iss = 2 * issued if issued else 2 * 1.03 * pf["flops"]
+            # same tiles as the float form: twice its issued FLOPs (the
+            # instruction counters give the same)
+            iss = ((mm or {}).get("f16_cache_1024", {}).get("issued_flops")
+                   or (2 * issued if issued else 2 * 1.03 * pf["flops"]))
             out["prefill"]["f16_cache_1024"] = {
                 "products": "f16 (v_mfma_f32_32x32x16_f16; the cache operand exact, Q and P as f16 pairs)",
                 "tflops_causal": round(pf["tflops"], 2), "us": round(pf["kernel_ms"] * 1e3, 2),
