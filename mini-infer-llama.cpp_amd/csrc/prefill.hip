@@ -64,18 +64,6 @@ typedef __attribute__((address_space(3))) unsigned lds_u32;
 
 namespace {
 
-// One element at byte offset vo (per lane, range-checked) + so (wave-uniform).
-template <typename KT>
-__device__ inline float load1(rsrc_t r, unsigned vo, unsigned so);
-template <>
-__device__ inline float load1<float>(rsrc_t r, unsigned vo, unsigned so) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
-}
-template <>
-__device__ inline float load1<_Float16>(rsrc_t r, unsigned vo, unsigned so) {
-  return (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0));
-}
-
 // 16 bytes per lane from r at vo (per lane, range-checked) + so (wave-uniform)
 // into LDS at lds + 16 * lane. (A plain function: in the kernel template the
 // host pass rejects the builtin's LDS pointer and drops the kernel silently.)
